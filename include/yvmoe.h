@@ -1,0 +1,197 @@
+/*
+ * yvmoe.h — C ABI of the MI355X (gfx950) Yv MoE layer inference forward.
+ *
+ * Every entry point takes raw device pointers and sizes, never allocates or frees device
+ * memory, launches only on the stream it is given (a hipStream_t passed as void*), and
+ * returns a yvmoe_status. yvmoe_last_error() returns a thread-local message for the last
+ * failure on the calling thread. Scratch memory comes from the caller as a workspace whose
+ * size yvmoe_workspace_bytes() reports.
+ *
+ * Reference interfaces replaced (Dunimd-Experimental/PiscesLx):
+ *   yvmoe_router_logits  -> YvStableMoEGate.gate(x_flat) and complexity_predictor(x)
+ *                           model/moe/gate.py:1179, :1112-1117, fixed mode :1148
+ *   yvmoe_route          -> YvStableMoEGate.forward after the logits (softmax, topk,
+ *                           double softmax, capacity trim) model/moe/gate.py:1147-1241,
+ *                           plus the sort / bincount / cumsum of
+ *                           PiscesLxFusedMoEDispatch.forward opss/infer/fused_moe.py:69-100
+ *   yvmoe_expert_ffn     -> the per-expert loop of PiscesLxFusedMoEDispatch.forward
+ *                           opss/infer/fused_moe.py:103-111 calling YvSwiGLUExpert.forward
+ *                           model/moe/expert.py:475-489, and the shared experts of
+ *                           YvDynamicMoELayer._compute_shared_expert_output
+ *                           model/moe/layer.py:812-865
+ *   yvmoe_combine        -> the index_add_ combine opss/infer/fused_moe.py:117-119, the
+ *                           routed + shared sum model/moe/layer.py:942-945 and
+ *                           _apply_skip_residual model/moe/layer.py:741-753
+ *   yvmoe_forward        -> YvDeepSeekMoELayer.forward / YvDynamicMoELayer.forward
+ *                           model/moe/layer.py:1283-1396 / :867-963 (inference)
+ */
+#ifndef YVMOE_H
+#define YVMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    YVMOE_OK = 0,
+    YVMOE_ERR_ARG = 1,         /* null pointer or value out of range */
+    YVMOE_ERR_SHAPE = 2,       /* sizes the kernels do not support (see limits below) */
+    YVMOE_ERR_DTYPE = 3,       /* unknown activation dtype or weight format */
+    YVMOE_ERR_UNSUPPORTED = 4, /* gate state the inference path rejects */
+    YVMOE_ERR_LAUNCH = 5,      /* a kernel launch failed */
+    YVMOE_ERR_WORKSPACE = 6    /* workspace missing or smaller than yvmoe_workspace_bytes */
+} yvmoe_status;
+
+/* activation dtype of x, the expert intermediates and the output */
+typedef enum { YVMOE_ACT_F32 = 0, YVMOE_ACT_BF16 = 1 } yvmoe_act_dtype;
+
+/* expert weight formats (all [out][in] row-major per expert, like nn.Linear.weight) */
+typedef enum {
+    YVMOE_W_F32 = 0,  /* fp32 weights, no scales (activations must be fp32) */
+    YVMOE_W_BF16 = 1, /* bf16 weights, no scales */
+    YVMOE_W_INT8 = 2, /* int8 symmetric per output channel: w = q * s, s bf16 [out] */
+    YVMOE_W_INT4 = 3, /* int4, group 128 along in, zero point 8: w = (q - 8) * s,
+                         two codes per byte, low nibble = even input index,
+                         s bf16 [out][in/128] */
+    YVMOE_W_FP8 = 4   /* fp8 e4m3fn (OCP), w = q * s, s fp32 per 128x128 block
+                         [out/128][in/128] */
+} yvmoe_weight_format;
+
+/* Limits checked on entry: 1 <= E <= 256, 1 <= k <= min(E, 16), 0 <= S <= 8,
+ * H and F multiples of 64 (of 128 for INT4 and FP8), N >= 0. */
+#define YVMOE_MAX_EXPERTS 256
+#define YVMOE_MAX_TOPK 16
+#define YVMOE_MAX_SHARED 8
+#define YVMOE_PREDICTOR_DIM 64
+
+/*
+ * Routed and shared expert weights, stacked: experts [0, E) are the routed experts,
+ * [E, E + S) the shared experts (model/moe/layer.py:665-705 keys
+ * experts.{e}.{gate,up,down}_proj.weight and shared_experts.{s}.expert.*).
+ *   w_gate, w_up : [E+S][F][H] elements of the format (INT4: [E+S][F][H/2] bytes)
+ *   w_down       : [E+S][H][F]                         (INT4: [E+S][H][F/2] bytes)
+ *   s_gate, s_up : INT8 bf16 [E+S][F]; INT4 bf16 [E+S][F][H/128];
+ *                  FP8 fp32 [E+S][F/128][H/128]; NULL otherwise
+ *   s_down       : INT8 bf16 [E+S][H]; INT4 bf16 [E+S][H][F/128];
+ *                  FP8 fp32 [E+S][H/128][F/128]; NULL otherwise
+ */
+typedef struct {
+    int32_t format; /* yvmoe_weight_format */
+    int32_t num_routed;
+    int32_t num_shared;
+    int32_t hidden;
+    int32_t ffn;
+    const void* w_gate;
+    const void* w_up;
+    const void* w_down;
+    const void* s_gate;
+    const void* s_up;
+    const void* s_down;
+} yvmoe_expert_weights;
+
+/*
+ * Router state of YvStableMoEGate (model/moe/gate.py:895-1028).
+ *   w_router : activations bf16 -> bf16 [Ep + 192][H] = [gate.weight padded to Ep rows;
+ *              W1 hi; W1 mid; W1 lo], where W1 = complexity_predictor[0].weight [64][H]
+ *              split into three bf16 terms whose sum is W1 exactly;
+ *              activations fp32 -> fp32 [Ep + 64][H] = [gate.weight padded; W1].
+ *              Ep = E rounded up to a multiple of 16 (padding rows are zero).
+ *   b1 [64], w2 [64], b2 [1] : the rest of complexity_predictor (fp32).
+ *   bias [E] or NULL : added to the logits before the softmax — expert_bias in
+ *              fixed_shape_mode (gate.py:1149), the load adjustment 0.1*(pred - recent)
+ *              otherwise (gate.py:1203-1204).
+ */
+typedef struct {
+    int32_t num_experts; /* E */
+    int32_t hidden;      /* H */
+    int32_t top_k;       /* k */
+    int32_t fixed_shape_mode;
+    int32_t dynamic_capacity; /* enable_dynamic_capacity */
+    int32_t min_capacity;
+    double capacity_factor; /* used when dynamic_capacity == 0 */
+    const void* w_router;
+    const float* b1;
+    const float* w2;
+    const float* b2;
+    const float* bias;
+} yvmoe_router;
+
+/*
+ * Routing results (device buffers, caller-allocated).
+ *   weights [N][k] fp32, indices [N][k] int64 : the gate's (weights, top_idx)
+ *   counts [E], offsets [E+1] int32 : bincount and exclusive prefix sum
+ *   perm [N*k] int32 : flat slot t*k+j at each expert-sorted position (stable argsort)
+ *   pos [N*k] int32  : inverse of perm
+ *   capacity [1] int32 : the capacity used (-1 in fixed_shape_mode)
+ */
+typedef struct {
+    float* weights;
+    int64_t* indices;
+    int32_t* counts;
+    int32_t* offsets;
+    int32_t* perm;
+    int32_t* pos;
+    int32_t* capacity;
+} yvmoe_routing;
+
+const char* yvmoe_last_error(void);
+int32_t yvmoe_version(void);
+
+/* Workspace bytes needed by yvmoe_route / yvmoe_expert_ffn / yvmoe_forward for N tokens. */
+size_t yvmoe_workspace_bytes(int32_t n_tokens, int32_t act_dtype, const yvmoe_router* router,
+                             const yvmoe_expert_weights* experts);
+
+/*
+ * logits_out [N][ld] fp32 with ld = Ep + 192 (bf16 x) or Ep + 64 (fp32 x): columns [0, E)
+ * are the gate logits, the rest the complexity predictor's first-layer terms.
+ */
+int32_t yvmoe_router_logits(const void* x, int32_t act_dtype, int32_t n_tokens,
+                            const yvmoe_router* router, float* logits_out, int32_t ld,
+                            void* stream);
+
+/*
+ * Routing from fp32 logits [N][ld] (the first E columns are used).
+ *   predictor : NULL, or the predictor columns of yvmoe_router_logits (row stride ld,
+ *               column offset Ep) — required when the capacity is dynamic and
+ *               capacity_override < 0.
+ *   capacity_override >= 0 replaces the computed capacity (ignored in fixed mode).
+ */
+int32_t yvmoe_route(const float* logits, int32_t ld, const float* predictor, int32_t n_tokens,
+                    const yvmoe_router* router, int32_t capacity_override, yvmoe_routing* out,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Grouped SwiGLU FFN of all routed slots and shared experts:
+ *   y [N*k + S*N][H] (activation dtype) — rows [0, N*k) in expert-sorted order (the
+ *   routing's perm), rows N*k + s*N + t for shared expert s and token t.
+ * Requires a routing computed with the same workspace.
+ */
+int32_t yvmoe_expert_ffn(const void* x, int32_t act_dtype, int32_t n_tokens, int32_t top_k,
+                         const yvmoe_expert_weights* experts, const yvmoe_routing* routing,
+                         void* y, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * out[t] = sum_j weights[t,j] * y[pos[t*k+j]] + shared[t] + 0.1 * skip[t], accumulated in
+ * fp32 and rounded once; shared[t] = sum_s mix[s] * y[N*k + s*N + t].
+ *   mix [S] fp32 = softmax(shared_expert_weight); skip (activation dtype [N][H]) or NULL;
+ *   shared_out [N][H] or NULL receives shared[t] (the next call's skip buffer).
+ */
+int32_t yvmoe_combine(const void* y, int32_t act_dtype, int32_t n_tokens, int32_t hidden,
+                      int32_t top_k, int32_t num_shared, const yvmoe_routing* routing,
+                      const float* mix, const void* skip, void* out, void* shared_out,
+                      void* stream);
+
+/* The whole layer: router logits, routing, expert FFN and combine. */
+int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
+                      const yvmoe_router* router, const yvmoe_expert_weights* experts,
+                      const float* mix, const void* skip, void* out, void* shared_out,
+                      yvmoe_routing* routing, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* YVMOE_H */

@@ -1,0 +1,223 @@
+/*
+ * CPU oracle for the Yv MoE routing step — TEST INFRASTRUCTURE ONLY.
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this
+ * library, and only as the checker (or the timed CPU baseline). The product path in
+ * pisceslx_amd/ never calls it.
+ *
+ * It restates, in plain C with no FMA contraction (build with -ffp-contract=off), the
+ * routing algorithm of the reference:
+ *   YvStableMoEGate.forward            model/moe/gate.py:1122-1247
+ *     fixed_shape_mode path             gate.py:1147-1160  (logits + expert_bias)
+ *     dynamic capacity                  gate.py:1096-1120, :1172-1176
+ *     softmax -> topk -> double softmax gate.py:1212-1223
+ *     capacity trim + renormalisation   gate.py:1224-1241
+ *     eps                               model/utils/safety.py:51-55 (fp32 -> 1e-8)
+ *   PiscesLxFusedMoEDispatch.forward   opss/infer/fused_moe.py:69-100
+ *     stable argsort / bincount / cumsum offsets
+ *
+ * The reference delegates softmax, topk and the sums to torch, whose last-bit behaviour
+ * is not specified. To make routing bit-exact between this oracle and the GPU kernel the
+ * build fixes those choices (the GPU kernel in pisceslx_amd/csrc/yvmoe_route.hip follows
+ * the same specification operation for operation):
+ *   - exp:      yv_expf below: Cody-Waite reduction with the Cephes expf split of ln2
+ *               (C1 = 0.693359375, C2 = -2.12194440e-4), degree-7 Taylor polynomial in
+ *               Horner form, exact scaling by 2^n; inputs below -86 give 0.
+ *   - softmax:  m = max_e z_e; ex_e = yv_expf(z_e - m); the sum uses 16 partial sums
+ *               (partial l accumulates e = l, l+16, l+32, ... in increasing e) folded by
+ *               a butterfly over xor offsets 8, 4, 2, 1; p_e = ex_e / sum (IEEE divide).
+ *   - topk:     k largest p, ordered by (p desc, expert index asc): ties go to the lower
+ *               expert index.
+ *   - weights:  w_j = yv_expf(ts_j - ts_0) / sum_j(...) with the sum taken sequentially
+ *               over j = 0..k-1 (softmax of the k top probabilities, gate.py:1223).
+ *   - capacity: for an expert with more than `cap` tokens, tokens are ranked by
+ *               (p[t,e] desc, token asc) and those past rank cap lose that slot
+ *               (torch.topk(largest=False) at gate.py:1234 leaves ties unspecified).
+ *   - renorm:   total = sequential sum over j; w_j = (w_j * a_j) / max(total, 1e-8),
+ *               and 0 when total == 0 (gate.py:1239-1241).
+ *
+ * Parity pins (tests/test_oracle_routing.py): yv_expf against libm exp within 2 ulp on a
+ * dense grid; the softmax against float64 within 4 ulp; topk against brute force over all
+ * C(E,k) subsets; the whole routing against a torch restatement of gate.py (indices
+ * identical, weights within 1e-6) on seeded inputs; the capacity rules against the
+ * reference test's invariants (tools/test/test_moe_routing_contract.py:84-112); the
+ * permutation against numpy's stable argsort.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define YV_LANES 16
+
+float yvo_expf(float x) {
+    if (!(x >= -86.0f)) return 0.0f; /* also maps NaN and -inf to 0 */
+    if (x > 88.0f) return INFINITY;
+    float fn = rintf(x * 1.44269504088896341f);
+    int n = (int)fn;
+    float r = x - fn * 0.693359375f;
+    r = r + fn * 2.12194440e-4f;
+    float p = 1.98412698e-4f;
+    p = p * r + 1.38888889e-3f;
+    p = p * r + 8.33333333e-3f;
+    p = p * r + 4.16666667e-2f;
+    p = p * r + 1.66666667e-1f;
+    p = p * r + 0.5f;
+    p = p * r + 1.0f;
+    p = p * r + 1.0f;
+    union { uint32_t u; float f; } s;
+    s.u = (uint32_t)(n + 127) << 23;
+    return p * s.f;
+}
+
+/* softmax over one row of E values (bias may be NULL), following the spec above. */
+void yvo_softmax_row(const float* z_in, const float* bias, int E, float* p) {
+    float m = -INFINITY;
+    for (int e = 0; e < E; ++e) {
+        float z = bias ? z_in[e] + bias[e] : z_in[e];
+        p[e] = z;
+        if (z > m) m = z;
+    }
+    float part[YV_LANES];
+    for (int l = 0; l < YV_LANES; ++l) part[l] = 0.0f;
+    for (int e = 0; e < E; ++e) {
+        float ex = yvo_expf(p[e] - m);
+        p[e] = ex;
+        part[e % YV_LANES] = part[e % YV_LANES] + ex;
+    }
+    for (int o = YV_LANES / 2; o >= 1; o >>= 1) {
+        float tmp[YV_LANES];
+        for (int l = 0; l < YV_LANES; ++l) tmp[l] = part[l] + part[l ^ o];
+        memcpy(part, tmp, sizeof part);
+    }
+    float s = part[0];
+    for (int e = 0; e < E; ++e) p[e] = p[e] / s;
+}
+
+/* topk of one probability row: (p desc, index asc). */
+void yvo_topk_row(const float* p, int E, int k, float* ts, int32_t* idx) {
+    for (int j = 0; j < k; ++j) {
+        int best = -1;
+        for (int e = 0; e < E; ++e) {
+            int taken = 0;
+            for (int i = 0; i < j; ++i) taken |= (idx[i] == e);
+            if (taken) continue;
+            if (best < 0 || p[e] > p[best]) best = e; /* strict: equal keeps lower index */
+        }
+        idx[j] = best;
+        ts[j] = p[best];
+    }
+}
+
+/* softmax of the k top probabilities (gate.py:1223). */
+void yvo_topk_weights(const float* ts, int k, float* w) {
+    float tot = 0.0f;
+    for (int j = 0; j < k; ++j) {
+        w[j] = yvo_expf(ts[j] - ts[0]);
+        tot = tot + w[j];
+    }
+    for (int j = 0; j < k; ++j) w[j] = w[j] / tot;
+}
+
+/* cap = max(int(N * cf / E), min_cap), cf = clamp(0.5 + 1.5 * avg, 0.5, 2.0) in double
+ * (gate.py:1117-1120, :1173-1176). */
+int yvo_capacity(float avg, int N, int E, int min_cap) {
+    double cf = 0.5 + 1.5 * (double)avg;
+    if (cf > 2.0) cf = 2.0;
+    if (cf < 0.5) cf = 0.5;
+    double c = (double)N * cf / (double)E;
+    int cap = (int)c;
+    return cap < min_cap ? min_cap : cap;
+}
+
+typedef struct { float p; int32_t t; int32_t slot; } yvo_cand;
+
+static int yvo_cand_cmp(const void* a, const void* b) {
+    const yvo_cand* x = (const yvo_cand*)a;
+    const yvo_cand* y = (const yvo_cand*)b;
+    if (x->p > y->p) return -1;
+    if (x->p < y->p) return 1;
+    return (x->t < y->t) ? -1 : (x->t > y->t);
+}
+
+/*
+ * Full routing of N tokens.
+ *   logits [N,E] fp32, bias [E] or NULL, cap < 0 disables the capacity trim.
+ * Outputs (all caller-allocated):
+ *   topp [N,k]   p of the chosen experts (the capacity ranking keys)
+ *   w0   [N,k]   double-softmax weights before the trim
+ *   w    [N,k]   final weights
+ *   idx  [N,k]   expert indices
+ *   allowed [N,k] 1 = kept, 0 = dropped by capacity
+ *   counts [E], offsets [E+1]
+ *   perm [N*k]   flat slot index at each expert-sorted position (stable)
+ *   pos  [N*k]   inverse of perm
+ * Returns 0, or -1 on bad arguments / allocation failure.
+ */
+int yvo_route(const float* logits, const float* bias, int N, int E, int k, int cap,
+              float* topp, float* w0, float* w, int32_t* idx, uint8_t* allowed,
+              int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* pos) {
+    if (N < 0 || E <= 0 || k <= 0 || k > E || k > 64) return -1;
+    float* p = (float*)malloc(sizeof(float) * (size_t)(E > 0 ? E : 1));
+    float* pall = (float*)malloc(sizeof(float) * (size_t)N * (size_t)E + 1);
+    if (!p || !pall) { free(p); free(pall); return -1; }
+    for (int t = 0; t < N; ++t) {
+        yvo_softmax_row(logits + (size_t)t * E, bias, E, pall + (size_t)t * E);
+        yvo_topk_row(pall + (size_t)t * E, E, k, topp + (size_t)t * k, idx + (size_t)t * k);
+        yvo_topk_weights(topp + (size_t)t * k, k, w0 + (size_t)t * k);
+    }
+    for (int e = 0; e < E; ++e) counts[e] = 0;
+    for (size_t s = 0; s < (size_t)N * k; ++s) { counts[idx[s]]++; allowed[s] = 1; }
+    offsets[0] = 0;
+    for (int e = 0; e < E; ++e) offsets[e + 1] = offsets[e] + counts[e];
+    /* stable counting sort of flat slots by expert */
+    int32_t* fill = (int32_t*)malloc(sizeof(int32_t) * (size_t)E);
+    if (!fill) { free(p); free(pall); return -1; }
+    memcpy(fill, offsets, sizeof(int32_t) * (size_t)E);
+    for (size_t s = 0; s < (size_t)N * k; ++s) {
+        int32_t q = fill[idx[s]]++;
+        perm[q] = (int32_t)s;
+        pos[s] = q;
+    }
+    free(fill);
+    if (cap >= 0) {
+        yvo_cand* c = (yvo_cand*)malloc(sizeof(yvo_cand) * (size_t)(N > 0 ? N : 1));
+        if (!c) { free(p); free(pall); return -1; }
+        for (int e = 0; e < E; ++e) {
+            int n = counts[e];
+            if (n <= cap) continue;
+            for (int i = 0; i < n; ++i) {
+                int32_t s = perm[offsets[e] + i];
+                c[i].slot = s;
+                c[i].t = s / k;
+                c[i].p = topp[s];
+            }
+            qsort(c, (size_t)n, sizeof(yvo_cand), yvo_cand_cmp);
+            for (int i = cap; i < n; ++i) allowed[c[i].slot] = 0;
+        }
+        free(c);
+    }
+    for (int t = 0; t < N; ++t) {
+        float tot = 0.0f;
+        float tmp[64];
+        for (int j = 0; j < k; ++j) {
+            tmp[j] = w0[(size_t)t * k + j] * (allowed[(size_t)t * k + j] ? 1.0f : 0.0f);
+            tot = tot + tmp[j];
+        }
+        float den = tot > 1e-8f ? tot : 1e-8f;
+        float keep = tot > 0.0f ? 1.0f : 0.0f;
+        for (int j = 0; j < k; ++j) w[(size_t)t * k + j] = (tmp[j] * keep) / den;
+    }
+    free(p);
+    free(pall);
+    return 0;
+}
+
+/* vectorised helpers for the tests */
+void yvo_expf_array(const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = yvo_expf(x[i]);
+}
+
+void yvo_softmax_rows(const float* z, const float* bias, int N, int E, float* p) {
+    for (int t = 0; t < N; ++t) yvo_softmax_row(z + (size_t)t * E, bias, E, p + (size_t)t * E);
+}

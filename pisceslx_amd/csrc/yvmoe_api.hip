@@ -1,0 +1,231 @@
+// extern "C" entry points of libyvmoe (declared in include/yvmoe.h): argument checks,
+// workspace carving and kernel sequencing. No entry point allocates device memory.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "yvmoe_internal.h"
+
+namespace yvmoe {
+
+static thread_local char g_err[512] = "";
+
+void set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+void clear_error() { g_err[0] = '\0'; }
+
+static int check_router(const yvmoe_router* r, int act) {
+    YV_REQUIRE(r != nullptr, YVMOE_ERR_ARG, "router is NULL");
+    YV_REQUIRE(r->num_experts >= 1 && r->num_experts <= YVMOE_MAX_EXPERTS, YVMOE_ERR_SHAPE,
+               "num_experts=%d outside [1, %d]", r->num_experts, YVMOE_MAX_EXPERTS);
+    YV_REQUIRE(r->top_k >= 1 && r->top_k <= r->num_experts && r->top_k <= YVMOE_MAX_TOPK,
+               YVMOE_ERR_SHAPE, "top_k=%d outside [1, min(E=%d, %d)]", r->top_k, r->num_experts,
+               YVMOE_MAX_TOPK);
+    YV_REQUIRE(act == YVMOE_ACT_F32 || act == YVMOE_ACT_BF16, YVMOE_ERR_DTYPE,
+               "unknown activation dtype %d", act);
+    YV_REQUIRE(r->min_capacity >= 0, YVMOE_ERR_ARG, "min_capacity=%d < 0", r->min_capacity);
+    return YVMOE_OK;
+}
+
+static int check_experts(const yvmoe_expert_weights* w, int act) {
+    YV_REQUIRE(w != nullptr, YVMOE_ERR_ARG, "expert weights are NULL");
+    YV_REQUIRE(w->num_routed >= 1 && w->num_routed <= YVMOE_MAX_EXPERTS, YVMOE_ERR_SHAPE,
+               "num_routed=%d outside [1, %d]", w->num_routed, YVMOE_MAX_EXPERTS);
+    YV_REQUIRE(w->num_shared >= 0 && w->num_shared <= YVMOE_MAX_SHARED, YVMOE_ERR_SHAPE,
+               "num_shared=%d outside [0, %d]", w->num_shared, YVMOE_MAX_SHARED);
+    YV_REQUIRE(w->hidden > 0 && w->hidden % 64 == 0 && w->ffn > 0 && w->ffn % 64 == 0,
+               YVMOE_ERR_SHAPE, "hidden=%d and ffn=%d must be positive multiples of 64",
+               w->hidden, w->ffn);
+    YV_REQUIRE(w->w_gate && w->w_up && w->w_down, YVMOE_ERR_ARG, "expert weight pointer is NULL");
+    switch (w->format) {
+        case YVMOE_W_F32:
+            YV_REQUIRE(act == YVMOE_ACT_F32, YVMOE_ERR_DTYPE, "fp32 weights need fp32 activations");
+            break;
+        case YVMOE_W_BF16:
+            YV_REQUIRE(act == YVMOE_ACT_BF16, YVMOE_ERR_DTYPE, "bf16 weights need bf16 activations");
+            break;
+        case YVMOE_W_INT8:
+        case YVMOE_W_INT4:
+        case YVMOE_W_FP8:
+            YV_REQUIRE(act == YVMOE_ACT_BF16, YVMOE_ERR_DTYPE,
+                       "quantized weights need bf16 activations");
+            YV_REQUIRE(w->s_gate && w->s_up && w->s_down, YVMOE_ERR_ARG,
+                       "quantized weights need scales");
+            if (w->format != YVMOE_W_INT8)
+                YV_REQUIRE(w->hidden % 128 == 0 && w->ffn % 128 == 0, YVMOE_ERR_SHAPE,
+                           "int4/fp8 need hidden=%d and ffn=%d multiples of 128", w->hidden, w->ffn);
+            break;
+        default:
+            set_error("unknown weight format %d", w->format);
+            return YVMOE_ERR_DTYPE;
+    }
+    return YVMOE_OK;
+}
+
+static int check_routing(const yvmoe_routing* o) {
+    YV_REQUIRE(o != nullptr && o->weights && o->indices && o->counts && o->offsets && o->perm &&
+                   o->pos && o->capacity,
+               YVMOE_ERR_ARG, "routing output pointer is NULL");
+    return YVMOE_OK;
+}
+
+}  // namespace yvmoe
+
+using namespace yvmoe;
+
+extern "C" {
+
+const char* yvmoe_last_error(void) { return g_err; }
+
+int32_t yvmoe_version(void) { return 1; }
+
+size_t yvmoe_workspace_bytes(int32_t n_tokens, int32_t act_dtype, const yvmoe_router* router,
+                             const yvmoe_expert_weights* experts) {
+    if (n_tokens < 0 || router == nullptr) return 0;
+    const int N = n_tokens, E = router->num_experts, k = router->top_k;
+    size_t total = route_ws(N, E, k).bytes;
+    if (experts != nullptr)
+        total += ffn_ws(N, k, experts->num_routed, experts->num_shared, experts->ffn, act_dtype).bytes;
+    total += align_up((size_t)N * router_ld(E, act_dtype) * 4, 256);
+    if (experts != nullptr)
+        total += y_bytes(N, k, experts->num_shared, experts->hidden, act_dtype);
+    return total;
+}
+
+int32_t yvmoe_router_logits(const void* x, int32_t act_dtype, int32_t n_tokens,
+                            const yvmoe_router* router, float* logits_out, int32_t ld,
+                            void* stream) {
+    clear_error();
+    int rc = check_router(router, act_dtype);
+    if (rc) return rc;
+    YV_REQUIRE(n_tokens >= 0, YVMOE_ERR_ARG, "n_tokens=%d < 0", n_tokens);
+    if (n_tokens == 0) return YVMOE_OK;
+    YV_REQUIRE(x && logits_out && router->w_router, YVMOE_ERR_ARG, "NULL pointer");
+    YV_REQUIRE(router->hidden > 0 && router->hidden % 64 == 0, YVMOE_ERR_SHAPE,
+               "hidden=%d must be a positive multiple of 64", router->hidden);
+    YV_REQUIRE(ld >= router_ld(router->num_experts, act_dtype), YVMOE_ERR_SHAPE,
+               "ld=%d smaller than %d", ld, router_ld(router->num_experts, act_dtype));
+    return router_gemm_launch(x, act_dtype, n_tokens, router, logits_out, ld, (hipStream_t)stream);
+}
+
+int32_t yvmoe_route(const float* logits, int32_t ld, const float* predictor, int32_t n_tokens,
+                    const yvmoe_router* router, int32_t capacity_override, yvmoe_routing* out,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = check_router(router, YVMOE_ACT_F32);
+    if (rc) return rc;
+    rc = check_routing(out);
+    if (rc) return rc;
+    YV_REQUIRE(n_tokens >= 0, YVMOE_ERR_ARG, "n_tokens=%d < 0", n_tokens);
+    YV_REQUIRE(n_tokens == 0 || logits, YVMOE_ERR_ARG, "logits are NULL");
+    YV_REQUIRE(ld >= router->num_experts, YVMOE_ERR_SHAPE, "ld=%d < E=%d", ld, router->num_experts);
+    YV_REQUIRE((long long)n_tokens * router->top_k < (1ll << 31), YVMOE_ERR_SHAPE,
+               "N*k overflows int32");
+    const size_t need = route_ws(n_tokens, router->num_experts, router->top_k).bytes;
+    YV_REQUIRE(workspace != nullptr && workspace_bytes >= need, YVMOE_ERR_WORKSPACE,
+               "workspace %zu bytes, need %zu", workspace_bytes, need);
+    // predictor columns: ld must be Ep + 64 * terms with terms 1 (fp32) or 3 (bf16)
+    const int pterms = (ld - pad16(router->num_experts)) / kPredDim;
+    if (predictor != nullptr)
+        YV_REQUIRE(pterms == 1 || pterms == 3, YVMOE_ERR_SHAPE,
+                   "predictor needs ld = Ep + 64 or Ep + 192, got %d", ld);
+    if (!router->fixed_shape_mode && router->dynamic_capacity && capacity_override < 0)
+        YV_REQUIRE(predictor && router->b1 && router->w2 && router->b2, YVMOE_ERR_ARG,
+                   "dynamic capacity needs the predictor columns and weights");
+    return route_launch(logits, ld, predictor, ld, n_tokens, router, capacity_override, out,
+                        (char*)workspace, (hipStream_t)stream);
+}
+
+int32_t yvmoe_expert_ffn(const void* x, int32_t act_dtype, int32_t n_tokens, int32_t top_k,
+                         const yvmoe_expert_weights* experts, const yvmoe_routing* routing,
+                         void* y, void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = check_experts(experts, act_dtype);
+    if (rc) return rc;
+    rc = check_routing(routing);
+    if (rc) return rc;
+    YV_REQUIRE(n_tokens >= 0, YVMOE_ERR_ARG, "n_tokens=%d < 0", n_tokens);
+    YV_REQUIRE(top_k >= 1 && top_k <= YVMOE_MAX_TOPK && top_k <= experts->num_routed,
+               YVMOE_ERR_SHAPE, "top_k=%d invalid", top_k);
+    if (n_tokens == 0) return YVMOE_OK;
+    YV_REQUIRE(x && y, YVMOE_ERR_ARG, "NULL pointer");
+    const long long rows = (long long)n_tokens * (top_k + experts->num_shared);
+    YV_REQUIRE(rows * experts->hidden < (1ll << 40), YVMOE_ERR_SHAPE, "problem too large");
+    const size_t need = route_ws(n_tokens, experts->num_routed, top_k).bytes +
+                        ffn_ws(n_tokens, top_k, experts->num_routed, experts->num_shared,
+                               experts->ffn, act_dtype).bytes;
+    YV_REQUIRE(workspace != nullptr && workspace_bytes >= need, YVMOE_ERR_WORKSPACE,
+               "workspace %zu bytes, need %zu", workspace_bytes, need);
+    return expert_ffn_launch(x, act_dtype, n_tokens, top_k, experts, routing, y, (char*)workspace,
+                             (hipStream_t)stream);
+}
+
+int32_t yvmoe_combine(const void* y, int32_t act_dtype, int32_t n_tokens, int32_t hidden,
+                      int32_t top_k, int32_t num_shared, const yvmoe_routing* routing,
+                      const float* mix, const void* skip, void* out, void* shared_out,
+                      void* stream) {
+    clear_error();
+    int rc = check_routing(routing);
+    if (rc) return rc;
+    YV_REQUIRE(act_dtype == YVMOE_ACT_F32 || act_dtype == YVMOE_ACT_BF16, YVMOE_ERR_DTYPE,
+               "unknown activation dtype %d", act_dtype);
+    YV_REQUIRE(n_tokens >= 0 && hidden > 0 && hidden % 8 == 0, YVMOE_ERR_SHAPE,
+               "bad n_tokens=%d / hidden=%d", n_tokens, hidden);
+    YV_REQUIRE(top_k >= 1 && top_k <= YVMOE_MAX_TOPK, YVMOE_ERR_SHAPE, "top_k=%d invalid", top_k);
+    YV_REQUIRE(num_shared >= 0 && num_shared <= YVMOE_MAX_SHARED, YVMOE_ERR_SHAPE,
+               "num_shared=%d invalid", num_shared);
+    YV_REQUIRE(num_shared == 0 || mix != nullptr, YVMOE_ERR_ARG, "shared experts need mix weights");
+    if (n_tokens == 0) return YVMOE_OK;
+    YV_REQUIRE(y && out, YVMOE_ERR_ARG, "NULL pointer");
+    return combine_launch(y, act_dtype, n_tokens, hidden, top_k, num_shared, routing, mix, skip,
+                          out, shared_out, (hipStream_t)stream);
+}
+
+int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
+                      const yvmoe_router* router, const yvmoe_expert_weights* experts,
+                      const float* mix, const void* skip, void* out, void* shared_out,
+                      yvmoe_routing* routing, void* workspace, size_t workspace_bytes,
+                      void* stream) {
+    clear_error();
+    int rc = check_router(router, act_dtype);
+    if (rc) return rc;
+    rc = check_experts(experts, act_dtype);
+    if (rc) return rc;
+    rc = check_routing(routing);
+    if (rc) return rc;
+    YV_REQUIRE(router->num_experts == experts->num_routed && router->hidden == experts->hidden,
+               YVMOE_ERR_SHAPE, "router (E=%d, H=%d) and experts (E=%d, H=%d) disagree",
+               router->num_experts, router->hidden, experts->num_routed, experts->hidden);
+    YV_REQUIRE(n_tokens >= 0, YVMOE_ERR_ARG, "n_tokens=%d < 0", n_tokens);
+    const size_t need = yvmoe_workspace_bytes(n_tokens, act_dtype, router, experts);
+    YV_REQUIRE(workspace != nullptr && workspace_bytes >= need, YVMOE_ERR_WORKSPACE,
+               "workspace %zu bytes, need %zu", workspace_bytes, need);
+    YV_REQUIRE(n_tokens == 0 || (x && out), YVMOE_ERR_ARG, "NULL pointer");
+    YV_REQUIRE(experts->num_shared == 0 || mix != nullptr, YVMOE_ERR_ARG,
+               "shared experts need mix weights");
+    hipStream_t st = (hipStream_t)stream;
+    const int N = n_tokens, E = router->num_experts, k = router->top_k;
+    const int ld = router_ld(E, act_dtype);
+    char* ws = (char*)workspace;
+    float* logits = (float*)(ws + route_ws(N, E, k).bytes +
+                             ffn_ws(N, k, E, experts->num_shared, experts->ffn, act_dtype).bytes);
+    if (N > 0) {
+        rc = router_gemm_launch(x, act_dtype, N, router, logits, ld, st);
+        if (rc) return rc;
+    }
+    const bool need_pred = !router->fixed_shape_mode && router->dynamic_capacity;
+    rc = route_launch(logits, ld, need_pred ? logits + pad16(E) : nullptr, ld, N, router, -1,
+                      routing, ws, st);
+    if (rc) return rc;
+    if (N == 0) return YVMOE_OK;
+    void* y = (char*)logits + align_up((size_t)N * ld * 4, 256);
+    rc = expert_ffn_launch(x, act_dtype, N, k, experts, routing, y, ws, st);
+    if (rc) return rc;
+    return combine_launch(y, act_dtype, N, experts->hidden, k, experts->num_shared, routing, mix,
+                          skip, out, shared_out, st);
+}
+
+}  // extern "C"

@@ -1,0 +1,717 @@
+// Expert GEMMs, router GEMM and combine of the Yv MoE layer for gfx950 (CDNA4).
+//
+// Reference: PiscesLxFusedMoEDispatch.forward opss/infer/fused_moe.py:54-123 (per-expert
+// loop and index_add_ combine), YvSwiGLUExpert.forward model/moe/expert.py:475-489,
+// YvDynamicMoELayer._compute_shared_expert_output model/moe/layer.py:812-865, the gate
+// projection model/moe/gate.py:1179 and the complexity predictor gate.py:1112-1117.
+//
+// Tiling. A work-group is 4 wavefronts. It owns one 64-row tile of one expert segment
+// (rows are expert-sorted slots; shared experts are extra segments of all N tokens) and
+// 4 * NCB * 16 output columns; each wavefront owns NCB 16-column blocks over the whole K
+// range and up to four 16-row MFMA blocks (only the row blocks that hold rows are
+// computed). The B operand (weights, [out][in] row-major as nn.Linear stores them) streams
+// from HBM with 16-byte loads per lane and is dequantized in registers to bf16; the A
+// operand (activations gathered through the permutation) comes through L1/L2.
+// MFMA: v_mfma_f32_16x16x32_bf16 for bf16 activations, v_mfma_f32_16x16x4_f32 for fp32.
+// Lane l holds A[row l%16][k-chunk l/16] and B[k-chunk l/16][col l%16]; the accumulator
+// holds D[row 4*(l/16)+i][col l%16]. Each lane loads 16 consecutive k (bf16 path) or 4
+// (fp32 path); the two (four) MFMAs of a k-step use the same k permutation for A and B,
+// which leaves the sum unchanged.
+#include "yvmoe_internal.h"
+
+namespace yvmoe {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+enum Epi { EPI_F32 = 0, EPI_SWIGLU = 1, EPI_DOWN = 2 };
+
+struct GemmParams {
+    const void* A;
+    int lda;
+    const int* rowmap;  // sorted row -> token for routed rows; nullptr: A row = row
+    int routed_rows;    // rows >= routed_rows are shared rows (token = (row - routed) % ntok)
+    int ntok;
+    const void* B0;
+    const void* B1;
+    const void* S0;
+    const void* S1;
+    long long b_stride;  // per expert, in elements (bytes for int4)
+    long long s_stride;  // per expert, in scale elements
+    int K;
+    int ncols;
+    void* out;
+    int ldo;
+    const int* tile_seg;
+    const int* tile_row0;
+    const int* ntiles;
+    const int* seg_start;
+    int nrows;  // rows when there is no tile table
+};
+
+__device__ __forceinline__ unsigned short f32_to_bf16_rne(float f) {
+    unsigned u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;  // NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (unsigned short)(u >> 16);
+}
+__device__ __forceinline__ float bf16_to_f32(unsigned short h) {
+    return __uint_as_float((unsigned)h << 16);
+}
+// Two floats that are exactly representable in bf16 -> packed pair (lo in bits 0..15).
+__device__ __forceinline__ unsigned pack_exact(float lo, float hi) {
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+union Frag16 {  // 16 bf16 = two MFMA operands
+    uint4 u[2];
+    bf16x8 v[2];
+};
+
+// -------------------------------------------------------------- B fragment loaders
+// Each loads the 16 k-values of one output column for this lane's k-chunk and returns
+// them as two bf16x8 operands (values exact: dequant scales are applied to accumulators).
+template <int WF>
+struct BLoad;
+
+template <>
+struct BLoad<YVMOE_W_BF16> {
+    typedef Frag16 Raw;
+    static __device__ __forceinline__ const char* ptr(const void* base, long long e_off, int n,
+                                                      int K, int kl) {
+        return (const char*)base + (e_off + (long long)n * K + kl) * 2;
+    }
+    static __device__ __forceinline__ void load(Raw& r, const char* p, int k0) {
+        const uint4* q = (const uint4*)(p + (size_t)k0 * 2);
+        r.u[0] = q[0];
+        r.u[1] = q[1];
+    }
+    static __device__ __forceinline__ void cvt(const Raw& r, Frag16& f) { f = r; }
+};
+
+template <>
+struct BLoad<YVMOE_W_INT8> {
+    typedef uint4 Raw;
+    static __device__ __forceinline__ const char* ptr(const void* base, long long e_off, int n,
+                                                      int K, int kl) {
+        return (const char*)base + (e_off + (long long)n * K + kl);
+    }
+    static __device__ __forceinline__ void load(Raw& r, const char* p, int k0) {
+        r = *(const uint4*)(p + k0);
+    }
+    static __device__ __forceinline__ void cvt(const Raw& r, Frag16& f) {
+        const unsigned w[4] = {r.x, r.y, r.z, r.w};
+        unsigned o[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float a = (float)(int)(signed char)(w[i] & 0xffu);
+            const float b = (float)(int)(signed char)((w[i] >> 8) & 0xffu);
+            const float c = (float)(int)(signed char)((w[i] >> 16) & 0xffu);
+            const float d = (float)((int)w[i] >> 24);
+            o[2 * i] = pack_exact(a, b);
+            o[2 * i + 1] = pack_exact(c, d);
+        }
+        f.u[0] = make_uint4(o[0], o[1], o[2], o[3]);
+        f.u[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+};
+
+template <>
+struct BLoad<YVMOE_W_INT4> {
+    typedef uint2 Raw;
+    static __device__ __forceinline__ const char* ptr(const void* base, long long e_off, int n,
+                                                      int K, int kl) {
+        return (const char*)base + e_off + ((long long)n * K + kl) / 2;
+    }
+    static __device__ __forceinline__ void load(Raw& r, const char* p, int k0) {
+        r = *(const uint2*)(p + k0 / 2);
+    }
+    static __device__ __forceinline__ void cvt(const Raw& r, Frag16& f) {
+        const unsigned w[2] = {r.x, r.y};
+        unsigned o[8];
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const unsigned byte = (w[i] >> (8 * j)) & 0xffu;  // low nibble = even k
+                const float lo = (float)((int)(byte & 0xfu) - 8);
+                const float hi = (float)((int)(byte >> 4) - 8);
+                o[4 * i + j] = pack_exact(lo, hi);
+            }
+        }
+        f.u[0] = make_uint4(o[0], o[1], o[2], o[3]);
+        f.u[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+};
+
+template <>
+struct BLoad<YVMOE_W_FP8> {
+    typedef uint4 Raw;
+    static __device__ __forceinline__ const char* ptr(const void* base, long long e_off, int n,
+                                                      int K, int kl) {
+        return (const char*)base + (e_off + (long long)n * K + kl);
+    }
+    static __device__ __forceinline__ void load(Raw& r, const char* p, int k0) {
+        r = *(const uint4*)(p + k0);
+    }
+    static __device__ __forceinline__ void cvt(const Raw& r, Frag16& f) {
+        const unsigned w[4] = {r.x, r.y, r.z, r.w};
+        unsigned o[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            // e4m3fn -> f32 is exact, and every e4m3fn value is exact in bf16
+            const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
+            const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
+            o[2 * i] = pack_exact(a.x, a.y);
+            o[2 * i + 1] = pack_exact(b.x, b.y);
+        }
+        f.u[0] = make_uint4(o[0], o[1], o[2], o[3]);
+        f.u[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+};
+
+__device__ __forceinline__ int map_row(const GemmParams& p, int row) {
+    if (p.rowmap == nullptr) return row;
+    if (row < p.routed_rows) return p.rowmap[row];
+    return (row - p.routed_rows) % p.ntok;
+}
+
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+
+// Column scale applied in the epilogue (int8 per-channel); 1 otherwise.
+template <int WF>
+__device__ __forceinline__ float col_scale(const void* S, long long e_off, int n) {
+    if constexpr (WF == YVMOE_W_INT8) {
+        return bf16_to_f32(((const unsigned short*)S)[e_off + n]);
+    } else {
+        return 1.0f;
+    }
+}
+
+// Group (128 along K) scale of column n, group g: int4 bf16 [n][K/128]; fp8 fp32 [n/128][K/128].
+template <int WF>
+__device__ __forceinline__ float group_scale(const void* S, long long e_off, int n, int K, int g) {
+    if constexpr (WF == YVMOE_W_INT4) {
+        return bf16_to_f32(((const unsigned short*)S)[e_off + (long long)n * (K / 128) + g]);
+    } else {
+        return ((const float*)S)[e_off + (long long)(n / 128) * (K / 128) + g];
+    }
+}
+
+template <int EPI>
+struct NMat {
+    static constexpr int value = (EPI == EPI_SWIGLU) ? 2 : 1;
+};
+
+// ------------------------------------------------------------------ bf16 activations
+template <int WF, int EPI, int NCB>
+__global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
+    constexpr int NM = NMat<EPI>::value;
+    constexpr bool GROUPED = (WF == YVMOE_W_INT4 || WF == YVMOE_W_FP8);
+    typedef BLoad<WF> BL;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int e = 0, row0, seg_end;
+    if (p.tile_seg != nullptr) {
+        const int tile = blockIdx.x;
+        if (tile >= *p.ntiles) return;
+        e = p.tile_seg[tile];
+        row0 = p.tile_row0[tile];
+        seg_end = p.seg_start[e + 1];
+    } else {
+        row0 = blockIdx.x * kTileRows;
+        if (row0 >= p.nrows) return;
+        seg_end = p.nrows;
+    }
+    const int col0 = (blockIdx.y * 4 + wave) * NCB * 16;
+    if (col0 >= p.ncols) return;
+    const int nrb = min(4, (seg_end - row0 + 15) / 16);
+    const int kl = (lane >> 4) * 16;  // this lane's k offset inside a 64-wide k-step
+
+    const char* arow[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+        int r = row0 + rb * 16 + (lane & 15);
+        if (r >= seg_end) r = row0;
+        arow[rb] = (const char*)p.A + ((long long)map_row(p, r) * p.lda + kl) * 2;
+    }
+    const long long e_off = (long long)e * p.b_stride;
+    const char* bptr[NM][NCB];
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+        const int n = col0 + cb * 16 + (lane & 15);
+        bptr[0][cb] = BL::ptr(p.B0, e_off, n, p.K, kl);
+        if constexpr (NM == 2) bptr[NM - 1][cb] = BL::ptr(p.B1, e_off, n, p.K, kl);
+    }
+
+    f32x4 acc[NM][NCB][4];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) acc[m][cb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int nks = p.K / 64;
+    typename BL::Raw braw[NM][NCB], bnext[NM][NCB];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb) BL::load(braw[m][cb], bptr[m][cb], 0);
+
+    f32x4 gacc[NM][NCB][4];
+    for (int ks = 0; ks < nks; ++ks) {
+        const int k0 = ks * 64;
+        if (ks + 1 < nks) {
+#pragma unroll
+            for (int m = 0; m < NM; ++m)
+#pragma unroll
+                for (int cb = 0; cb < NCB; ++cb) BL::load(bnext[m][cb], bptr[m][cb], k0 + 64);
+        }
+        Frag16 af[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            if (rb < nrb) {
+                const uint4* q = (const uint4*)(arow[rb] + (size_t)k0 * 2);
+                af[rb].u[0] = q[0];
+                af[rb].u[1] = q[1];
+            }
+        }
+        if constexpr (GROUPED) {
+            if ((ks & 1) == 0) {
+#pragma unroll
+                for (int m = 0; m < NM; ++m)
+#pragma unroll
+                    for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+                        for (int rb = 0; rb < 4; ++rb) gacc[m][cb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < NM; ++m) {
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) {
+                Frag16 bf;
+                BL::cvt(braw[m][cb], bf);
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    if (rb < nrb) {
+                        f32x4& dst = GROUPED ? gacc[m][cb][rb] : acc[m][cb][rb];
+                        dst = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[rb].v[0], bf.v[0], dst, 0, 0, 0);
+                        dst = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[rb].v[1], bf.v[1], dst, 0, 0, 0);
+                    }
+                }
+            }
+        }
+        if constexpr (GROUPED) {
+            if ((ks & 1) == 1) {
+                const int g = ks >> 1;
+#pragma unroll
+                for (int m = 0; m < NM; ++m) {
+                    const void* S = (m == 0) ? p.S0 : p.S1;
+#pragma unroll
+                    for (int cb = 0; cb < NCB; ++cb) {
+                        const int n = col0 + cb * 16 + (lane & 15);
+                        const float s = group_scale<WF>(S, (long long)e * p.s_stride, n, p.K, g);
+#pragma unroll
+                        for (int rb = 0; rb < 4; ++rb) {
+                            if (rb < nrb) {
+#pragma unroll
+                                for (int i = 0; i < 4; ++i)
+                                    acc[m][cb][rb][i] = acc[m][cb][rb][i] + gacc[m][cb][rb][i] * s;
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        if (ks + 1 < nks) {
+#pragma unroll
+            for (int m = 0; m < NM; ++m)
+#pragma unroll
+                for (int cb = 0; cb < NCB; ++cb) braw[m][cb] = bnext[m][cb];
+        }
+    }
+
+    // epilogue
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+        const int n = col0 + cb * 16 + (lane & 15);
+        const long long so = (long long)e * p.s_stride;
+        const float s0 = col_scale<WF>(p.S0, so, n);
+        float s1 = 1.0f;
+        if constexpr (NM == 2) s1 = col_scale<WF>(p.S1, so, n);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            if (rb < nrb) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = row0 + rb * 16 + (lane >> 4) * 4 + i;
+                    if (r < seg_end) {
+                        if constexpr (EPI == EPI_F32) {
+                            ((float*)p.out)[(long long)r * p.ldo + n] = acc[0][cb][rb][i];
+                        } else if constexpr (EPI == EPI_SWIGLU) {
+                            const float g = acc[0][cb][rb][i] * s0;
+                            const float u = acc[NM - 1][cb][rb][i] * s1;
+                            ((unsigned short*)p.out)[(long long)r * p.ldo + n] =
+                                f32_to_bf16_rne(silu(g) * u);
+                        } else {
+                            ((unsigned short*)p.out)[(long long)r * p.ldo + n] =
+                                f32_to_bf16_rne(acc[0][cb][rb][i] * s0);
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ fp32 activations
+// fp32 activations and fp32 weights (the reference's fp32 configuration).
+template <int EPI, int NCB>
+__global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
+    constexpr int NM = NMat<EPI>::value;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    int e = 0, row0, seg_end;
+    if (p.tile_seg != nullptr) {
+        const int tile = blockIdx.x;
+        if (tile >= *p.ntiles) return;
+        e = p.tile_seg[tile];
+        row0 = p.tile_row0[tile];
+        seg_end = p.seg_start[e + 1];
+    } else {
+        row0 = blockIdx.x * kTileRows;
+        if (row0 >= p.nrows) return;
+        seg_end = p.nrows;
+    }
+    const int col0 = (blockIdx.y * 4 + wave) * NCB * 16;
+    if (col0 >= p.ncols) return;
+    const int nrb = min(4, (seg_end - row0 + 15) / 16);
+    const int kl = (lane >> 4) * 4;
+    const float* arow[4];
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+        int r = row0 + rb * 16 + (lane & 15);
+        if (r >= seg_end) r = row0;
+        arow[rb] = (const float*)p.A + (long long)map_row(p, r) * p.lda + kl;
+    }
+    const long long e_off = (long long)e * p.b_stride;
+    const float* bptr[NM][NCB];
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+        const int n = col0 + cb * 16 + (lane & 15);
+        bptr[0][cb] = (const float*)p.B0 + e_off + (long long)n * p.K + kl;
+        if constexpr (NM == 2) bptr[NM - 1][cb] = (const float*)p.B1 + e_off + (long long)n * p.K + kl;
+    }
+    f32x4 acc[NM][NCB][4];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb) acc[m][cb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int k0 = 0; k0 < p.K; k0 += 16) {
+        float4 bv[NM][NCB];
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) bv[m][cb] = *(const float4*)(bptr[m][cb] + k0);
+        float4 av[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb)
+            if (rb < nrb) av[rb] = *(const float4*)(arow[rb] + k0);
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb)
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) {
+                    if (rb < nrb) {
+                        f32x4& d = acc[m][cb][rb];
+                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(av[rb].x, bv[m][cb].x, d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(av[rb].y, bv[m][cb].y, d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(av[rb].z, bv[m][cb].z, d, 0, 0, 0);
+                        d = __builtin_amdgcn_mfma_f32_16x16x4f32(av[rb].w, bv[m][cb].w, d, 0, 0, 0);
+                    }
+                }
+    }
+#pragma unroll
+    for (int cb = 0; cb < NCB; ++cb) {
+        const int n = col0 + cb * 16 + (lane & 15);
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            if (rb < nrb) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = row0 + rb * 16 + (lane >> 4) * 4 + i;
+                    if (r < seg_end) {
+                        float v;
+                        if constexpr (EPI == EPI_SWIGLU) v = silu(acc[0][cb][rb][i]) * acc[NM - 1][cb][rb][i];
+                        else v = acc[0][cb][rb][i];
+                        ((float*)p.out)[(long long)r * p.ldo + n] = v;
+                    }
+                }
+            }
+        }
+    }
+}
+
+// --------------------------------------------------------------- tile schedule
+// Segments: routed experts [0, E) from the routing offsets, then S shared experts of N
+// rows each after the N*k routed rows. Every segment is cut into 64-row tiles.
+__global__ __launch_bounds__(512) void build_tiles_kernel(const int* __restrict__ offsets, int E,
+                                                          int S, int N, int k, int* __restrict__ seg,
+                                                          int* __restrict__ tile_seg,
+                                                          int* __restrict__ tile_row0,
+                                                          int* __restrict__ ntiles) {
+    __shared__ int sc[512];
+    const int tid = threadIdx.x;
+    const int nseg = E + S;
+    int s0 = 0, s1 = 0, nt = 0;
+    if (tid < nseg) {
+        if (tid < E) {
+            s0 = offsets[tid];
+            s1 = offsets[tid + 1];
+        } else {
+            s0 = N * k + (tid - E) * N;
+            s1 = s0 + N;
+        }
+        seg[tid] = s0;
+        if (tid == nseg - 1) seg[nseg] = s1;
+        nt = (s1 - s0 + kTileRows - 1) / kTileRows;
+    }
+    sc[tid] = nt;
+    __syncthreads();
+    for (int o = 1; o < 512; o <<= 1) {
+        int v = (tid >= o) ? sc[tid - o] : 0;
+        __syncthreads();
+        sc[tid] += v;
+        __syncthreads();
+    }
+    if (tid < nseg) {
+        const int start = sc[tid] - nt;
+        for (int q = 0; q < nt; ++q) {
+            tile_seg[start + q] = tid;
+            tile_row0[start + q] = s0 + q * kTileRows;
+        }
+    }
+    if (tid == 511) *ntiles = sc[511];
+}
+
+// --------------------------------------------------------------- combine
+// out[t] = round( (sum_j w[t,j] * y[pos[t,j]] + shared[t]) + 0.1 * skip[t] ), fp32 sums in
+// a fixed order (deterministic, unlike the reference's atomic index_add_ on GPU).
+template <int ACT>
+__global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y, int N, int H,
+                                                      int k, int S, const float* __restrict__ w,
+                                                      const int* __restrict__ pos,
+                                                      const float* __restrict__ mix,
+                                                      const void* __restrict__ skip,
+                                                      void* __restrict__ out,
+                                                      void* __restrict__ shared_out) {
+    constexpr int VEC = (ACT == YVMOE_ACT_BF16) ? 8 : 4;
+    const int t = blockIdx.y;
+    const int h = (blockIdx.x * blockDim.x + threadIdx.x) * VEC;
+    if (h >= H) return;
+    float acc[VEC], sh[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) {
+        acc[v] = 0.0f;
+        sh[v] = 0.0f;
+    }
+    auto load = [&](long long row, float* dst) {
+        if constexpr (ACT == YVMOE_ACT_BF16) {
+            const uint4 q = *(const uint4*)((const unsigned short*)y + row * H + h);
+            const unsigned u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                dst[2 * i] = __uint_as_float(u[i] << 16);
+                dst[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+            }
+        } else {
+            const float4 q = *(const float4*)((const float*)y + row * H + h);
+            dst[0] = q.x;
+            dst[1] = q.y;
+            dst[2] = q.z;
+            dst[3] = q.w;
+        }
+    };
+    float tmp[VEC];
+    for (int j = 0; j < k; ++j) {
+        const float wj = w[(long long)t * k + j];
+        load(pos[(long long)t * k + j], tmp);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) acc[v] = acc[v] + wj * tmp[v];
+    }
+    for (int s = 0; s < S; ++s) {
+        const float ms = mix[s];
+        load((long long)N * k + (long long)s * N + t, tmp);
+#pragma unroll
+        for (int v = 0; v < VEC; ++v) sh[v] = sh[v] + ms * tmp[v];
+    }
+    float o[VEC];
+#pragma unroll
+    for (int v = 0; v < VEC; ++v) o[v] = acc[v] + sh[v];
+    if (skip != nullptr) {
+        if constexpr (ACT == YVMOE_ACT_BF16) {
+            const uint4 q = *(const uint4*)((const unsigned short*)skip + (long long)t * H + h);
+            const unsigned u[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                o[2 * i] = o[2 * i] + 0.1f * __uint_as_float(u[i] << 16);
+                o[2 * i + 1] = o[2 * i + 1] + 0.1f * __uint_as_float(u[i] & 0xffff0000u);
+            }
+        } else {
+            const float4 q = *(const float4*)((const float*)skip + (long long)t * H + h);
+            o[0] = o[0] + 0.1f * q.x;
+            o[1] = o[1] + 0.1f * q.y;
+            o[2] = o[2] + 0.1f * q.z;
+            o[3] = o[3] + 0.1f * q.w;
+        }
+    }
+    if constexpr (ACT == YVMOE_ACT_BF16) {
+        unsigned pk[4], ps[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pk[i] = (unsigned)f32_to_bf16_rne(o[2 * i]) | ((unsigned)f32_to_bf16_rne(o[2 * i + 1]) << 16);
+            ps[i] = (unsigned)f32_to_bf16_rne(sh[2 * i]) | ((unsigned)f32_to_bf16_rne(sh[2 * i + 1]) << 16);
+        }
+        *(uint4*)((unsigned short*)out + (long long)t * H + h) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        if (shared_out != nullptr)
+            *(uint4*)((unsigned short*)shared_out + (long long)t * H + h) = make_uint4(ps[0], ps[1], ps[2], ps[3]);
+    } else {
+        *(float4*)((float*)out + (long long)t * H + h) = make_float4(o[0], o[1], o[2], o[3]);
+        if (shared_out != nullptr)
+            *(float4*)((float*)shared_out + (long long)t * H + h) = make_float4(sh[0], sh[1], sh[2], sh[3]);
+    }
+}
+
+// Picks NCB so that every wavefront's columns are in range, and launches.
+template <int EPI>
+int gemm_dispatch(int act, int wf, GemmParams p, int ntiles_max, hipStream_t st,
+                  const char* name) {
+    const int ncb = (p.ncols % 32 == 0) ? 2 : 1;
+    const int cols_per_wg = 4 * ncb * 16;
+    dim3 grid(ntiles_max, (p.ncols + cols_per_wg - 1) / cols_per_wg);
+    if (ntiles_max <= 0) return YVMOE_OK;
+    if (act == YVMOE_ACT_F32) {
+        if (ncb == 2) gemm_f32_kernel<EPI, 2><<<grid, 256, 0, st>>>(p);
+        else gemm_f32_kernel<EPI, 1><<<grid, 256, 0, st>>>(p);
+    } else {
+#define YV_GB(WFV)                                                          \
+    do {                                                                    \
+        if (ncb == 2) gemm_bf16_kernel<WFV, EPI, 2><<<grid, 256, 0, st>>>(p); \
+        else gemm_bf16_kernel<WFV, EPI, 1><<<grid, 256, 0, st>>>(p);        \
+    } while (0)
+        switch (wf) {
+            case YVMOE_W_BF16: YV_GB(YVMOE_W_BF16); break;
+            case YVMOE_W_INT8: YV_GB(YVMOE_W_INT8); break;
+            case YVMOE_W_INT4: YV_GB(YVMOE_W_INT4); break;
+            case YVMOE_W_FP8: YV_GB(YVMOE_W_FP8); break;
+            default: set_error("unsupported weight format %d for bf16 activations", wf); return YVMOE_ERR_DTYPE;
+        }
+#undef YV_GB
+    }
+    YV_LAUNCH_CHECK(name);
+    return YVMOE_OK;
+}
+
+}  // namespace
+
+int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, float* out, int ld,
+                       hipStream_t st) {
+    GemmParams p{};
+    p.A = x;
+    p.lda = r->hidden;
+    p.rowmap = nullptr;
+    p.B0 = r->w_router;
+    p.K = r->hidden;
+    p.ncols = router_ld(r->num_experts, act);
+    p.out = out;
+    p.ldo = ld;
+    p.nrows = N;
+    const int wf = (act == YVMOE_ACT_F32) ? YVMOE_W_F32 : YVMOE_W_BF16;
+    return gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), st, "router_gemm");
+}
+
+int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_weights* w,
+                      const yvmoe_routing* routing, void* y, char* ws, hipStream_t st) {
+    const int E = w->num_routed, S = w->num_shared, H = w->hidden, F = w->ffn;
+    const RouteWs RL = route_ws(N, E, k);
+    const FfnWs FL = ffn_ws(N, k, E, S, F, act);
+    char* fws = ws + RL.bytes;
+    int* seg = (int*)(fws + FL.seg);
+    int* tile_seg = (int*)(fws + FL.tile_seg);
+    int* tile_row0 = (int*)(fws + FL.tile_row0);
+    int* ntiles = (int*)(fws + FL.ntiles);
+    void* hbuf = fws + FL.h;
+    const int T = max_tiles(N, k, E, S);
+    build_tiles_kernel<<<1, 512, 0, st>>>(routing->offsets, E, S, N, k, seg, tile_seg, tile_row0,
+                                          ntiles);
+    YV_LAUNCH_CHECK("build_tiles");
+    const int wf = w->format;
+    GemmParams p{};
+    p.tile_seg = tile_seg;
+    p.tile_row0 = tile_row0;
+    p.ntiles = ntiles;
+    p.seg_start = seg;
+    // GEMM1: h = silu(x Wg^T) * (x Wu^T) over gathered rows
+    p.A = x;
+    p.lda = H;
+    p.rowmap = (const int*)(ws + RL.tok);
+    p.routed_rows = N * k;
+    p.ntok = N;
+    p.B0 = w->w_gate;
+    p.B1 = w->w_up;
+    p.S0 = w->s_gate;
+    p.S1 = w->s_up;
+    p.b_stride = (long long)F * H;
+    if (wf == YVMOE_W_INT8) p.s_stride = F;
+    else if (wf == YVMOE_W_INT4) p.s_stride = (long long)F * (H / 128);
+    else if (wf == YVMOE_W_FP8) p.s_stride = (long long)(F / 128) * (H / 128);
+    p.K = H;
+    p.ncols = F;
+    p.out = hbuf;
+    p.ldo = F;
+    int rc = gemm_dispatch<EPI_SWIGLU>(act, wf, p, T, st, "expert_gemm1");
+    if (rc != YVMOE_OK) return rc;
+    // GEMM2: y = h Wd^T (rows already in sorted order)
+    p.A = hbuf;
+    p.lda = F;
+    p.rowmap = nullptr;
+    p.B0 = w->w_down;
+    p.B1 = nullptr;
+    p.S0 = w->s_down;
+    p.S1 = nullptr;
+    p.b_stride = (long long)H * F;
+    if (wf == YVMOE_W_INT8) p.s_stride = H;
+    else if (wf == YVMOE_W_INT4) p.s_stride = (long long)H * (F / 128);
+    else if (wf == YVMOE_W_FP8) p.s_stride = (long long)(H / 128) * (F / 128);
+    p.K = F;
+    p.ncols = H;
+    p.out = y;
+    p.ldo = H;
+    return gemm_dispatch<EPI_DOWN>(act, wf, p, T, st, "expert_gemm2");
+}
+
+int combine_launch(const void* y, int act, int N, int H, int k, int S, const yvmoe_routing* routing,
+                   const float* mix, const void* skip, void* out, void* shared_out, hipStream_t st) {
+    if (N == 0) return YVMOE_OK;
+    const int vec = (act == YVMOE_ACT_BF16) ? 8 : 4;
+    dim3 grid(ceil_div(H / vec, 256), N);
+    if (act == YVMOE_ACT_BF16)
+        combine_kernel<YVMOE_ACT_BF16><<<grid, 256, 0, st>>>(y, N, H, k, S, routing->weights,
+                                                             routing->pos, mix, skip, out,
+                                                             S > 0 ? shared_out : nullptr);
+    else
+        combine_kernel<YVMOE_ACT_F32><<<grid, 256, 0, st>>>(y, N, H, k, S, routing->weights,
+                                                            routing->pos, mix, skip, out,
+                                                            S > 0 ? shared_out : nullptr);
+    YV_LAUNCH_CHECK("combine");
+    return YVMOE_OK;
+}
+
+}  // namespace yvmoe

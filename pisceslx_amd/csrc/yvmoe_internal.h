@@ -1,0 +1,112 @@
+// Internal declarations shared by the yvmoe HIP translation units (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/yvmoe.h"
+
+namespace yvmoe {
+
+// ---------------------------------------------------------------- error reporting
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define YV_REQUIRE(cond, code, ...)          \
+    do {                                     \
+        if (!(cond)) {                       \
+            ::yvmoe::set_error(__VA_ARGS__); \
+            return (code);                   \
+        }                                    \
+    } while (0)
+
+#define YV_LAUNCH_CHECK(name)                                                          \
+    do {                                                                               \
+        hipError_t e_ = hipGetLastError();                                             \
+        if (e_ != hipSuccess) {                                                        \
+            ::yvmoe::set_error("%s launch failed: %s", name, hipGetErrorString(e_));   \
+            return YVMOE_ERR_LAUNCH;                                                   \
+        }                                                                              \
+    } while (0)
+
+// ---------------------------------------------------------------- sizes
+constexpr int kTokPerBlock = 64;  // tokens per routing block
+constexpr int kTileRows = 64;     // rows per expert GEMM tile (4 MFMA row blocks)
+constexpr int kPredDim = YVMOE_PREDICTOR_DIM;
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+inline int ceil_div(int a, int b) { return (a + b - 1) / b; }
+inline int pad16(int e) { return (e + 15) / 16 * 16; }
+
+// Router output row stride for an activation dtype.
+inline int router_ld(int E, int act) {
+    return pad16(E) + (act == YVMOE_ACT_BF16 ? 3 * kPredDim : kPredDim);
+}
+
+// Upper bound on the number of 64-row GEMM tiles over all segments.
+inline int max_tiles(int N, int k, int E, int S) {
+    return ceil_div(N * k, kTileRows) + E + S * ceil_div(N, kTileRows);
+}
+
+// Workspace layout. The routing region depends on (N, E, k) only, so yvmoe_route and
+// yvmoe_expert_ffn agree on it without knowing each other's arguments.
+struct RouteWs {
+    size_t topp, w0, allowed, blockhist, blockoff, blocksum, tok, bytes;
+};
+struct FfnWs {
+    size_t seg, tile_seg, tile_row0, ntiles, h, bytes;
+};
+
+inline RouteWs route_ws(int N, int E, int k) {
+    RouteWs w{};
+    const int nb = ceil_div(N, kTokPerBlock) > 0 ? ceil_div(N, kTokPerBlock) : 1;
+    size_t o = 0;
+    const size_t nk = (size_t)N * k;
+    w.topp = o;      o = align_up(o + nk * 4, 256);
+    w.w0 = o;        o = align_up(o + nk * 4, 256);
+    w.allowed = o;   o = align_up(o + nk, 256);
+    w.blockhist = o; o = align_up(o + (size_t)nb * E * 4, 256);
+    w.blockoff = o;  o = align_up(o + (size_t)nb * E * 4, 256);
+    w.blocksum = o;  o = align_up(o + (size_t)nb * 4, 256);
+    w.tok = o;       o = align_up(o + nk * 4 + 4, 256);
+    w.bytes = o;
+    return w;
+}
+
+inline FfnWs ffn_ws(int N, int k, int E, int S, int F, int act) {
+    FfnWs w{};
+    const size_t R = (size_t)N * k + (size_t)S * N;
+    const int T = max_tiles(N, k, E, S);
+    size_t o = 0;
+    w.seg = o;       o = align_up(o + (size_t)(E + S + 1) * 4, 256);
+    w.tile_seg = o;  o = align_up(o + (size_t)T * 4 + 4, 256);
+    w.tile_row0 = o; o = align_up(o + (size_t)T * 4 + 4, 256);
+    w.ntiles = o;    o = align_up(o + 4, 256);
+    const size_t esz = act == YVMOE_ACT_BF16 ? 2 : 4;
+    w.h = o;         o = align_up(o + R * (size_t)F * esz, 256);
+    w.bytes = o;
+    return w;
+}
+
+// Expert output rows [N*k + S*N][H] (yvmoe_forward keeps them in its workspace).
+inline size_t y_bytes(int N, int k, int S, int H, int act) {
+    const size_t R = (size_t)N * k + (size_t)S * N;
+    return align_up(R * (size_t)H * (act == YVMOE_ACT_BF16 ? 2 : 4), 256);
+}
+
+// ---------------------------------------------------------------- launchers
+// routing (yvmoe_route.hip)
+int route_launch(const float* logits, int ld, const float* pred, int pred_ld, int N,
+                 const yvmoe_router* r, int cap_override, yvmoe_routing* out, char* ws,
+                 hipStream_t st);
+// GEMMs and combine (yvmoe_gemm.hip)
+int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, float* out,
+                       int ld, hipStream_t st);
+int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_weights* w,
+                      const yvmoe_routing* routing, void* y, char* ws, hipStream_t st);
+int combine_launch(const void* y, int act, int N, int H, int k, int S,
+                   const yvmoe_routing* routing, const float* mix, const void* skip,
+                   void* out, void* shared_out, hipStream_t st);
+
+}  // namespace yvmoe

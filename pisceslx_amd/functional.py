@@ -1,0 +1,196 @@
+"""Functional entry points over libyvmoe: torch allocates, the HIP library computes.
+
+Every function runs on the tensors' CUDA (HIP) device and on torch's current stream; none
+of them has a CPU or PyTorch fallback — a call on CPU tensors raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .quant import PackedExperts
+
+
+def _act(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return _lib.ACT_BF16
+    if dtype == torch.float32:
+        return _lib.ACT_F32
+    raise ValueError(f"activation dtype {dtype} is not supported (bfloat16 or float32)")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_cuda(*ts: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("libyvmoe computes on the GPU only: got a CPU tensor")
+        if not t.is_contiguous():
+            raise ValueError("libyvmoe needs contiguous tensors")
+        dev = t.device
+    return dev
+
+
+def router_ld(num_experts: int, act: int) -> int:
+    ep = (num_experts + 15) // 16 * 16
+    return ep + (3 if act == _lib.ACT_BF16 else 1) * _lib.PREDICTOR_DIM
+
+
+@dataclass
+class RouterState:
+    """Device tensors of one YvStableMoEGate, packed for the router GEMM."""
+
+    num_experts: int
+    hidden: int
+    top_k: int
+    fixed_shape_mode: bool
+    dynamic_capacity: bool
+    min_capacity: int
+    capacity_factor: float
+    w_router: torch.Tensor
+    b1: Optional[torch.Tensor]
+    w2: Optional[torch.Tensor]
+    b2: Optional[torch.Tensor]
+    bias: Optional[torch.Tensor]
+
+    def struct(self) -> _lib.Router:
+        return _lib.Router(self.num_experts, self.hidden, self.top_k, int(self.fixed_shape_mode),
+                           int(self.dynamic_capacity), self.min_capacity, float(self.capacity_factor),
+                           _ptr(self.w_router), _ptr(self.b1), _ptr(self.w2), _ptr(self.b2),
+                           _ptr(self.bias))
+
+
+@dataclass
+class Routing:
+    weights: torch.Tensor   # [N, k] fp32
+    indices: torch.Tensor   # [N, k] int64
+    counts: torch.Tensor    # [E] int32
+    offsets: torch.Tensor   # [E+1] int32
+    perm: torch.Tensor      # [N*k] int32
+    pos: torch.Tensor       # [N*k] int32
+    capacity: torch.Tensor  # [1] int32
+
+    @staticmethod
+    def empty(N: int, E: int, k: int, device) -> "Routing":
+        i32 = dict(dtype=torch.int32, device=device)
+        return Routing(torch.empty(N, k, dtype=torch.float32, device=device),
+                       torch.empty(N, k, dtype=torch.int64, device=device),
+                       torch.empty(E, **i32), torch.empty(E + 1, **i32),
+                       torch.empty(N * k, **i32), torch.empty(N * k, **i32),
+                       torch.empty(1, **i32))
+
+    def struct(self) -> _lib.Routing:
+        return _lib.Routing(self.weights.data_ptr(), self.indices.data_ptr(), self.counts.data_ptr(),
+                            self.offsets.data_ptr(), self.perm.data_ptr(), self.pos.data_ptr(),
+                            self.capacity.data_ptr())
+
+
+def workspace_bytes(n_tokens: int, act: int, router: RouterState,
+                    experts: Optional[PackedExperts] = None) -> int:
+    r = router.struct()
+    e = experts.struct() if experts is not None else None
+    return int(_lib.lib().yvmoe_workspace_bytes(n_tokens, act, ctypes.byref(r),
+                                                ctypes.byref(e) if e is not None else None))
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+    return torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+
+
+def router_logits(x2d: torch.Tensor, router: RouterState) -> torch.Tensor:
+    """[N, ld] fp32: gate logits in columns [0, E), predictor first-layer terms after Ep."""
+    dev = _require_cuda(x2d, router.w_router)
+    act = _act(x2d.dtype)
+    N = x2d.shape[0]
+    ld = router_ld(router.num_experts, act)
+    out = torch.empty(N, ld, dtype=torch.float32, device=dev)
+    r = router.struct()
+    _lib.check(_lib.lib().yvmoe_router_logits(x2d.data_ptr(), act, N, ctypes.byref(r),
+                                               out.data_ptr(), ld, _stream(dev)),
+               "yvmoe_router_logits")
+    return out
+
+
+def route(logits: torch.Tensor, router: RouterState, predictor: bool = True,
+          capacity_override: int = -1) -> Routing:
+    """Routing from fp32 logits [N, ld] (first E columns are the gate logits).
+
+    ``predictor`` says the predictor columns follow at column Ep (as router_logits returns);
+    pass False for plain [N, E] logits together with a capacity override or a fixed-mode gate.
+    """
+    dev = _require_cuda(logits)
+    if logits.dtype != torch.float32:
+        raise ValueError("routing needs fp32 logits")
+    N, ld = logits.shape
+    E, k = router.num_experts, router.top_k
+    out = Routing.empty(N, E, k, dev)
+    ws = _workspace(workspace_bytes(N, _lib.ACT_F32, router), dev)
+    r = router.struct()
+    o = out.struct()
+    Ep = (E + 15) // 16 * 16
+    pred_ptr = logits.data_ptr() + Ep * 4 if (predictor and N > 0) else None
+    _lib.check(_lib.lib().yvmoe_route(logits.data_ptr() if N > 0 else None, ld, pred_ptr, N,
+                                       ctypes.byref(r), capacity_override, ctypes.byref(o),
+                                       ws.data_ptr(), ws.numel(), _stream(dev)), "yvmoe_route")
+    return out
+
+
+def expert_ffn(x2d: torch.Tensor, experts: PackedExperts, routing: Routing, top_k: int,
+               workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """y [N*k + S*N, H]: expert outputs in expert-sorted order, then the shared experts."""
+    dev = _require_cuda(x2d, *experts.tensors())
+    act = _act(x2d.dtype)
+    N = x2d.shape[0]
+    R = N * top_k + experts.num_shared * N
+    y = torch.empty(R, experts.hidden, dtype=x2d.dtype, device=dev)
+    e = experts.struct()
+    o = routing.struct()
+    if workspace is None:
+        raise ValueError("expert_ffn needs the workspace the routing was computed in")
+    _lib.check(_lib.lib().yvmoe_expert_ffn(x2d.data_ptr(), act, N, top_k, ctypes.byref(e),
+                                            ctypes.byref(o), y.data_ptr(), workspace.data_ptr(),
+                                            workspace.numel(), _stream(dev)), "yvmoe_expert_ffn")
+    return y
+
+
+def moe_forward(x2d: torch.Tensor, router: RouterState, experts: PackedExperts,
+                mix: Optional[torch.Tensor], skip: Optional[torch.Tensor],
+                workspace: Optional[torch.Tensor] = None):
+    """Whole layer. Returns (out [N,H], shared_out [N,H] or None, Routing)."""
+    dev = _require_cuda(x2d, router.w_router, mix, skip, *experts.tensors())
+    act = _act(x2d.dtype)
+    N, H = x2d.shape
+    if H != experts.hidden or H != router.hidden:
+        raise ValueError(f"hidden size {H} does not match the layer ({experts.hidden})")
+    E, k, S = router.num_experts, router.top_k, experts.num_shared
+    routing = Routing.empty(N, E, k, dev)
+    out = torch.empty_like(x2d)
+    shared_out = torch.empty_like(x2d) if S > 0 else None
+    need = workspace_bytes(N, act, router, experts)
+    if workspace is None or workspace.numel() < need:
+        workspace = _workspace(need, dev)
+    if skip is not None and (skip.shape != x2d.shape or skip.dtype != x2d.dtype):
+        raise ValueError("skip buffer must match x")
+    if mix is not None and (mix.dtype != torch.float32 or mix.numel() != S):
+        raise ValueError("mix must be fp32 [S]")
+    r = router.struct()
+    e = experts.struct()
+    o = routing.struct()
+    _lib.check(_lib.lib().yvmoe_forward(x2d.data_ptr(), act, N, ctypes.byref(r), ctypes.byref(e),
+                                         _ptr(mix), _ptr(skip), out.data_ptr(), _ptr(shared_out),
+                                         ctypes.byref(o), workspace.data_ptr(), workspace.numel(),
+                                         _stream(dev)), "yvmoe_forward")
+    return out, shared_out, routing

@@ -1,0 +1,112 @@
+"""Yv MoE layer forward on the GPU against the CPU oracle.
+
+For every configuration (full size where the CPU oracle finishes in seconds, reduced N /
+expert count otherwise) the GPU gate logits are checked against float64, the device
+capacity against the oracle's, the routing bit for bit given the GPU's fp32 logits, and
+the outputs against the oracle's reference forward: bf16 max-abs <= 2e-2 and cosine >=
+0.9999; fp32 max-abs <= 1e-4 and cosine >= 0.999999.
+"""
+import numpy as np
+import pytest
+import torch
+
+from pisceslx_amd import functional as yvf
+from pisceslx_amd.workloads import make_workload, mix_weights, router_state
+
+from helpers import cosine, max_abs, oracle_params
+
+pytestmark = pytest.mark.gpu
+
+BF16_MAX_ABS, BF16_COS = 2e-2, 0.9999
+F32_MAX_ABS, F32_COS = 1e-4, 0.999999
+
+
+def _tol(dtype):
+    return (F32_MAX_ABS, F32_COS) if dtype == torch.float32 else (BF16_MAX_ABS, BF16_COS)
+
+
+def _run_and_check(oracle, w, skip=None, tokens=None):
+    spec = w.spec
+    print(f"layer {spec.name} N={w.n_tokens} H={spec.hidden} E={spec.num_experts} "
+          f"F={spec.ffn} fmt={spec.fmt}", flush=True)
+    st = router_state(w)
+    mix = mix_weights(w)
+    x = w.x
+    logits = yvf.router_logits(x, st)
+    out, shared, routing = yvf.moe_forward(x, st, w.experts, mix, skip)
+    torch.cuda.synchronize()
+    E, k = spec.num_experts, spec.top_k
+    lg = logits[:, :E].cpu().numpy()
+    xc = x.cpu()
+    ref_lg = oracle.router_logits(xc, w.gate_weight.cpu())
+    np.testing.assert_allclose(lg, ref_lg, rtol=0, atol=2e-4 * max(1.0, np.abs(ref_lg).max()))
+    params = oracle_params(w)
+    cap = int(routing.capacity.item())
+    if spec.fixed_shape_mode:
+        assert cap == -1
+    else:
+        assert cap == oracle.layer_capacity(params, xc)
+    o = oracle.layer_forward(xc, params, logits=lg, cap=cap,
+                             skip=None if skip is None else skip.cpu(), tokens=tokens)
+    r = o["routing"]
+    assert np.array_equal(routing.indices.cpu().numpy(), r.indices.astype(np.int64))
+    assert np.array_equal(routing.weights.cpu().numpy().view(np.uint32), r.weights.view(np.uint32))
+    assert np.array_equal(routing.perm.cpu().numpy(), r.perm)
+    assert np.array_equal(routing.counts.cpu().numpy(), r.counts)
+    got = out.cpu()
+    want = o["out"]
+    if tokens is not None:
+        got, want = got[tokens], want[tokens]
+    tol_abs, tol_cos = _tol(x.dtype)
+    ma, cs = max_abs(got, want), cosine(got, want)
+    print(f"  out max_abs={ma:.3e} cos={cs:.7f}", flush=True)
+    assert ma <= tol_abs and cs >= tol_cos
+    if spec.num_shared > 0:
+        gs, ws = shared.cpu(), o["shared"]
+        if tokens is not None:
+            gs, ws = gs[tokens], ws[tokens]
+        assert max_abs(gs, ws) <= tol_abs and cosine(gs, ws) >= tol_cos
+    return out, shared, routing
+
+
+@pytest.mark.parametrize("name,kw", [
+    ("cfg1", {}),
+    ("cfg2", {}),
+    ("cfg3", {"n_tokens": 512}),
+    ("cfg4", {"n_tokens": 384}),
+    ("cfg5", {"n_tokens": 384, "num_experts": 32}),
+])
+def test_layer_matches_oracle(cuda, oracle, name, kw):
+    w = make_workload(name, device="cuda", **kw)
+    _run_and_check(oracle, w)
+
+
+def test_layer_with_skip_buffer(cuda, oracle):
+    w = make_workload("cfg2", device="cuda", n_tokens=40)
+    skip = torch.randn(40, w.spec.hidden, device="cuda").to(torch.bfloat16)
+    _run_and_check(oracle, w, skip=skip)
+
+
+def test_cfg3_full_size_sampled_tokens(cuda, oracle):
+    w = make_workload("cfg3", device="cuda")
+    rng = np.random.default_rng(0)
+    tokens = np.sort(rng.choice(w.n_tokens, 96, replace=False))
+    _run_and_check(oracle, w, tokens=tokens)
+
+
+def test_bf16_and_small_shapes(cuda, oracle):
+    # unquantized bf16 experts on a small layer, ragged odd lengths
+    from pisceslx_amd import _lib
+    from pisceslx_amd.workloads import LayerSpec
+    spec = LayerSpec("tiny_bf16", 256, 384, 12, 3, 1, _lib.W_BF16, torch.bfloat16)
+    w = make_workload(spec, device="cuda", lengths=[37, 1, 90])
+    _run_and_check(oracle, w)
+
+
+def test_forward_is_deterministic(cuda, oracle):
+    w = make_workload("cfg3", device="cuda", n_tokens=700)
+    st = router_state(w)
+    mix = mix_weights(w)
+    a = yvf.moe_forward(w.x, st, w.experts, mix, None)[0]
+    b = yvf.moe_forward(w.x, st, w.experts, mix, None)[0]
+    assert torch.equal(a, b)
