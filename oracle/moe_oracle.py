@@ -215,12 +215,12 @@ def layer_forward(x2d: torch.Tensor, params: LayerParams, logits: Optional[np.nd
         bias = None if params.bias is None else params.bias.float().numpy()
         routing = route(logits, k, c, bias)
     # dispatch (fused_moe.py:83-119): stable sort by expert, loop over active experts
-    acc = torch.zeros(N, H, dtype=torch.float32)
     token_of = routing.perm // k
     keep = np.ones(N, dtype=bool)
     if tokens is not None:
         keep[:] = False
         keep[np.asarray(tokens)] = True
+    Y = torch.zeros(N * k, H, dtype=torch.float32)   # expert outputs in expert-sorted order
     for e in range(E):
         a, b = int(routing.offsets[e]), int(routing.offsets[e + 1])
         sel = np.arange(a, b)[keep[token_of[a:b]]]
@@ -229,22 +229,32 @@ def layer_forward(x2d: torch.Tensor, params: LayerParams, logits: Optional[np.nd
         rows = torch.from_numpy(token_of[sel].astype(np.int64))
         wg, wu, wd = params.expert(e)
         ye = swiglu(x2d[rows], wg.to(dtype), wu.to(dtype), wd.to(dtype))
-        slots = torch.from_numpy(routing.perm[sel].astype(np.int64))
-        wts = torch.from_numpy(routing.weights.reshape(-1))[slots]
-        acc.index_add_(0, rows, wts[:, None] * ye.float())
+        Y[torch.from_numpy(sel)] = ye.float()
+    # weighted combine (fused_moe.py:117-119): per token, slots j = 0..k-1 in order,
+    # multiply then add in fp32 (the reference's GPU index_add_ is atomic and unordered)
+    acc = torch.zeros(N, H, dtype=torch.float32)
+    pos = torch.from_numpy(routing.pos.reshape(N, k).astype(np.int64))
+    wts = torch.from_numpy(routing.weights.reshape(N, k))
+    for j in range(k):
+        acc = acc + wts[:, j:j + 1] * Y[pos[:, j]]
+    # the routed sum accumulates in fp32 and is rounded once to the layer dtype (the
+    # reference's index_add_ of fp32 weights into a bf16 output is undefined); the shared
+    # mixture and the residual adds are tensor ops of the layer dtype (layer.py:859-863,
+    # :942-945, :750-752), rounded after every step
+    out = acc.to(dtype)
     shared = None
     if S > 0:
-        mix = F.softmax(params.mix_param.detach(), dim=0).float()
-        shared = torch.zeros(N, H, dtype=torch.float32)
+        mix = F.softmax(params.mix_param.detach(), dim=0)
+        shared = torch.zeros(N, H, dtype=dtype)
         rows = torch.from_numpy(np.nonzero(keep)[0])
         for s in range(S):
             wg, wu, wd = params.expert(E + s)
             wf = torch.cat([wg, wu], dim=0).to(dtype)  # layer.py:844 fused gate/up
             g, u = F.linear(x2d[rows], wf).chunk(2, dim=-1)
             so = F.linear(F.silu(g) * u, wd.to(dtype))
-            shared[rows] = shared[rows] + mix[s] * so.float()
-        acc = acc + shared
+            shared[rows] = shared[rows] + mix[s].to(dtype) * so
+        out = out + shared
         if skip is not None and tuple(skip.shape) == (N, H):
-            acc = acc + 0.1 * skip.float()
-    return {"out": acc.to(dtype), "shared": None if shared is None else shared.to(dtype),
+            out = out + 0.1 * skip.to(dtype)
+    return {"out": out, "shared": shared,
             "routing": routing, "logits": logits}

@@ -33,7 +33,8 @@
  *   - capacity: for an expert with more than `cap` tokens, tokens are ranked by
  *               (p[t,e] desc, token asc) and those past rank cap lose that slot
  *               (torch.topk(largest=False) at gate.py:1234 leaves ties unspecified).
- *   - renorm:   total = sequential sum over j; w_j = (w_j * a_j) / max(total, 1e-8),
+ *   - renorm:   (capacity mode only; fixed mode returns the weights as they are)
+ *               total = sequential sum over j; w_j = (w_j * a_j) / max(total, 1e-8),
  *               and 0 when total == 0 (gate.py:1239-1241).
  *
  * Parity pins (tests/test_oracle_routing.py): yv_expf against libm exp within 2 ulp on a
@@ -196,6 +197,13 @@ int yvo_route(const float* logits, const float* bias, int N, int E, int k, int c
             for (int i = cap; i < n; ++i) allowed[c[i].slot] = 0;
         }
         free(c);
+    }
+    if (cap < 0) {
+        /* fixed_shape_mode returns the double-softmax weights as they are (gate.py:1151-1160) */
+        memcpy(w, w0, sizeof(float) * (size_t)N * (size_t)k);
+        free(p);
+        free(pall);
+        return 0;
     }
     for (int t = 0; t < N; ++t) {
         float tot = 0.0f;

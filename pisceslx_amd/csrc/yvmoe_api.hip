@@ -65,10 +65,13 @@ static int check_experts(const yvmoe_expert_weights* w, int act) {
     return YVMOE_OK;
 }
 
-static int check_routing(const yvmoe_routing* o) {
-    YV_REQUIRE(o != nullptr && o->weights && o->indices && o->counts && o->offsets && o->perm &&
-                   o->pos && o->capacity,
-               YVMOE_ERR_ARG, "routing output pointer is NULL");
+// With no tokens only counts, offsets and capacity are written (zero-size tensors may
+// legitimately carry NULL data pointers).
+static int check_routing(const yvmoe_routing* o, int n_tokens) {
+    YV_REQUIRE(o != nullptr && o->counts && o->offsets && o->capacity, YVMOE_ERR_ARG,
+               "routing output pointer is NULL");
+    YV_REQUIRE(n_tokens == 0 || (o->weights && o->indices && o->perm && o->pos), YVMOE_ERR_ARG,
+               "routing output pointer is NULL");
     return YVMOE_OK;
 }
 
@@ -117,7 +120,7 @@ int32_t yvmoe_route(const float* logits, int32_t ld, const float* predictor, int
     clear_error();
     int rc = check_router(router, YVMOE_ACT_F32);
     if (rc) return rc;
-    rc = check_routing(out);
+    rc = check_routing(out, n_tokens);
     if (rc) return rc;
     YV_REQUIRE(n_tokens >= 0, YVMOE_ERR_ARG, "n_tokens=%d < 0", n_tokens);
     YV_REQUIRE(n_tokens == 0 || logits, YVMOE_ERR_ARG, "logits are NULL");
@@ -145,7 +148,7 @@ int32_t yvmoe_expert_ffn(const void* x, int32_t act_dtype, int32_t n_tokens, int
     clear_error();
     int rc = check_experts(experts, act_dtype);
     if (rc) return rc;
-    rc = check_routing(routing);
+    rc = check_routing(routing, n_tokens);
     if (rc) return rc;
     YV_REQUIRE(n_tokens >= 0, YVMOE_ERR_ARG, "n_tokens=%d < 0", n_tokens);
     YV_REQUIRE(top_k >= 1 && top_k <= YVMOE_MAX_TOPK && top_k <= experts->num_routed,
@@ -168,7 +171,7 @@ int32_t yvmoe_combine(const void* y, int32_t act_dtype, int32_t n_tokens, int32_
                       const float* mix, const void* skip, void* out, void* shared_out,
                       void* stream) {
     clear_error();
-    int rc = check_routing(routing);
+    int rc = check_routing(routing, n_tokens);
     if (rc) return rc;
     YV_REQUIRE(act_dtype == YVMOE_ACT_F32 || act_dtype == YVMOE_ACT_BF16, YVMOE_ERR_DTYPE,
                "unknown activation dtype %d", act_dtype);
@@ -194,7 +197,7 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
     if (rc) return rc;
     rc = check_experts(experts, act_dtype);
     if (rc) return rc;
-    rc = check_routing(routing);
+    rc = check_routing(routing, n_tokens);
     if (rc) return rc;
     YV_REQUIRE(router->num_experts == experts->num_routed && router->hidden == experts->hidden,
                YVMOE_ERR_SHAPE, "router (E=%d, H=%d) and experts (E=%d, H=%d) disagree",

@@ -12,6 +12,13 @@
 // computed). The B operand (weights, [out][in] row-major as nn.Linear stores them) streams
 // from HBM with 16-byte loads per lane and is dequantized in registers to bf16; the A
 // operand (activations gathered through the permutation) comes through L1/L2.
+//
+// Rounding points follow the reference's bf16 path, because the reference's own bf16
+// chain sits about 2e-2 (max-abs) from exact arithmetic at these shapes and a more exact
+// chain would not stay within that distance of it: weights are dequantized to
+// bf16(q * s) before the product (the reference dequantizes, then runs F.linear in bf16);
+// gate and up outputs, silu(gate), the product h and the down output are each rounded to
+// bf16 (YvSwiGLUExpert.forward, model/moe/expert.py:484-489). Products accumulate in fp32.
 // MFMA: v_mfma_f32_16x16x32_bf16 for bf16 activations, v_mfma_f32_16x16x4_f32 for fp32.
 // Lane l holds A[row l%16][k-chunk l/16] and B[k-chunk l/16][col l%16]; the accumulator
 // holds D[row 4*(l/16)+i][col l%16]. Each lane loads 16 consecutive k (bf16 path) or 4
@@ -25,6 +32,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
 enum Epi { EPI_F32 = 0, EPI_SWIGLU = 1, EPI_DOWN = 2 };
 
@@ -38,7 +46,7 @@ struct GemmParams {
     const void* B1;
     const void* S0;
     const void* S1;
-    long long b_stride;  // per expert, in elements (bytes for int4)
+    long long b_stride;  // per expert, in weight elements (int4: codes, two per byte)
     long long s_stride;  // per expert, in scale elements
     int K;
     int ncols;
@@ -51,19 +59,18 @@ struct GemmParams {
     int nrows;  // rows when there is no tile table
 };
 
+// Round-to-nearest-even fp32 -> bf16 pair (v_cvt_pk_bf16_f32), lo in bits 0..15.
+__device__ __forceinline__ unsigned pack_bf16(float lo, float hi) {
+    const bf16x2 v = __builtin_convertvector(f32x2{lo, hi}, bf16x2);
+    return __builtin_bit_cast(unsigned, v);
+}
 __device__ __forceinline__ unsigned short f32_to_bf16_rne(float f) {
-    unsigned u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0;  // NaN
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (unsigned short)(u >> 16);
+    return (unsigned short)(pack_bf16(f, 0.0f) & 0xffffu);
 }
 __device__ __forceinline__ float bf16_to_f32(unsigned short h) {
     return __uint_as_float((unsigned)h << 16);
 }
-// Two floats that are exactly representable in bf16 -> packed pair (lo in bits 0..15).
-__device__ __forceinline__ unsigned pack_exact(float lo, float hi) {
-    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
-}
+__device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16_rne(f)); }
 
 union Frag16 {  // 16 bf16 = two MFMA operands
     uint4 u[2];
@@ -72,7 +79,7 @@ union Frag16 {  // 16 bf16 = two MFMA operands
 
 // -------------------------------------------------------------- B fragment loaders
 // Each loads the 16 k-values of one output column for this lane's k-chunk and returns
-// them as two bf16x8 operands (values exact: dequant scales are applied to accumulators).
+// them as two bf16x8 operands holding bf16(q * s) (the reference's dequantized weights).
 template <int WF>
 struct BLoad;
 
@@ -88,7 +95,7 @@ struct BLoad<YVMOE_W_BF16> {
         r.u[0] = q[0];
         r.u[1] = q[1];
     }
-    static __device__ __forceinline__ void cvt(const Raw& r, Frag16& f) { f = r; }
+    static __device__ __forceinline__ void cvt(const Raw& r, float, Frag16& f) { f = r; }
 };
 
 template <>
@@ -101,7 +108,7 @@ struct BLoad<YVMOE_W_INT8> {
     static __device__ __forceinline__ void load(Raw& r, const char* p, int k0) {
         r = *(const uint4*)(p + k0);
     }
-    static __device__ __forceinline__ void cvt(const Raw& r, Frag16& f) {
+    static __device__ __forceinline__ void cvt(const Raw& r, float s, Frag16& f) {
         const unsigned w[4] = {r.x, r.y, r.z, r.w};
         unsigned o[8];
 #pragma unroll
@@ -110,8 +117,8 @@ struct BLoad<YVMOE_W_INT8> {
             const float b = (float)(int)(signed char)((w[i] >> 8) & 0xffu);
             const float c = (float)(int)(signed char)((w[i] >> 16) & 0xffu);
             const float d = (float)((int)w[i] >> 24);
-            o[2 * i] = pack_exact(a, b);
-            o[2 * i + 1] = pack_exact(c, d);
+            o[2 * i] = pack_bf16(a * s, b * s);
+            o[2 * i + 1] = pack_bf16(c * s, d * s);
         }
         f.u[0] = make_uint4(o[0], o[1], o[2], o[3]);
         f.u[1] = make_uint4(o[4], o[5], o[6], o[7]);
@@ -123,12 +130,13 @@ struct BLoad<YVMOE_W_INT4> {
     typedef uint2 Raw;
     static __device__ __forceinline__ const char* ptr(const void* base, long long e_off, int n,
                                                       int K, int kl) {
-        return (const char*)base + e_off + ((long long)n * K + kl) / 2;
+        // e_off, n * K and kl count int4 elements (all even): two per byte
+        return (const char*)base + (e_off + (long long)n * K + kl) / 2;
     }
     static __device__ __forceinline__ void load(Raw& r, const char* p, int k0) {
         r = *(const uint2*)(p + k0 / 2);
     }
-    static __device__ __forceinline__ void cvt(const Raw& r, Frag16& f) {
+    static __device__ __forceinline__ void cvt(const Raw& r, float s, Frag16& f) {
         const unsigned w[2] = {r.x, r.y};
         unsigned o[8];
 #pragma unroll
@@ -138,7 +146,7 @@ struct BLoad<YVMOE_W_INT4> {
                 const unsigned byte = (w[i] >> (8 * j)) & 0xffu;  // low nibble = even k
                 const float lo = (float)((int)(byte & 0xfu) - 8);
                 const float hi = (float)((int)(byte >> 4) - 8);
-                o[4 * i + j] = pack_exact(lo, hi);
+                o[4 * i + j] = pack_bf16(lo * s, hi * s);
             }
         }
         f.u[0] = make_uint4(o[0], o[1], o[2], o[3]);
@@ -156,16 +164,17 @@ struct BLoad<YVMOE_W_FP8> {
     static __device__ __forceinline__ void load(Raw& r, const char* p, int k0) {
         r = *(const uint4*)(p + k0);
     }
-    static __device__ __forceinline__ void cvt(const Raw& r, Frag16& f) {
+    static __device__ __forceinline__ void cvt(const Raw& r, float s, Frag16& f) {
         const unsigned w[4] = {r.x, r.y, r.z, r.w};
         unsigned o[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            // e4m3fn -> f32 is exact, and every e4m3fn value is exact in bf16
+            // e4m3fn -> f32 is exact; q * s is rounded in fp32, then to bf16 (as the reference's
+            // fp32 dequant followed by the cast to bf16)
             const f32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], false);
             const f32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8((int)w[i], true);
-            o[2 * i] = pack_exact(a.x, a.y);
-            o[2 * i + 1] = pack_exact(b.x, b.y);
+            o[2 * i] = pack_bf16(a.x * s, a.y * s);
+            o[2 * i + 1] = pack_bf16(b.x * s, b.y * s);
         }
         f.u[0] = make_uint4(o[0], o[1], o[2], o[3]);
         f.u[1] = make_uint4(o[4], o[5], o[6], o[7]);
@@ -178,25 +187,20 @@ __device__ __forceinline__ int map_row(const GemmParams& p, int row) {
     return (row - p.routed_rows) % p.ntok;
 }
 
-__device__ __forceinline__ float silu(float g) { return g / (1.0f + __expf(-g)); }
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
 
-// Column scale applied in the epilogue (int8 per-channel); 1 otherwise.
+// Dequant scale of column n for the k-step starting at k0: int8 bf16 [n]; int4 bf16
+// [n][K/128]; fp8 fp32 [n/128][K/128]; 1 for unscaled formats.
 template <int WF>
-__device__ __forceinline__ float col_scale(const void* S, long long e_off, int n) {
+__device__ __forceinline__ float b_scale(const void* S, long long e_off, int n, int K, int k0) {
     if constexpr (WF == YVMOE_W_INT8) {
         return bf16_to_f32(((const unsigned short*)S)[e_off + n]);
+    } else if constexpr (WF == YVMOE_W_INT4) {
+        return bf16_to_f32(((const unsigned short*)S)[e_off + (long long)n * (K / 128) + k0 / 128]);
+    } else if constexpr (WF == YVMOE_W_FP8) {
+        return ((const float*)S)[e_off + (long long)(n / 128) * (K / 128) + k0 / 128];
     } else {
         return 1.0f;
-    }
-}
-
-// Group (128 along K) scale of column n, group g: int4 bf16 [n][K/128]; fp8 fp32 [n/128][K/128].
-template <int WF>
-__device__ __forceinline__ float group_scale(const void* S, long long e_off, int n, int K, int g) {
-    if constexpr (WF == YVMOE_W_INT4) {
-        return bf16_to_f32(((const unsigned short*)S)[e_off + (long long)n * (K / 128) + g]);
-    } else {
-        return ((const float*)S)[e_off + (long long)(n / 128) * (K / 128) + g];
     }
 }
 
@@ -238,12 +242,15 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
         arow[rb] = (const char*)p.A + ((long long)map_row(p, r) * p.lda + kl) * 2;
     }
     const long long e_off = (long long)e * p.b_stride;
+    const long long s_off = (long long)e * p.s_stride;
     const char* bptr[NM][NCB];
+    const void* sptr[2] = {p.S0, p.S1};
+    int ncol[NCB];
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
-        const int n = col0 + cb * 16 + (lane & 15);
-        bptr[0][cb] = BL::ptr(p.B0, e_off, n, p.K, kl);
-        if constexpr (NM == 2) bptr[NM - 1][cb] = BL::ptr(p.B1, e_off, n, p.K, kl);
+        ncol[cb] = col0 + cb * 16 + (lane & 15);
+        bptr[0][cb] = BL::ptr(p.B0, e_off, ncol[cb], p.K, kl);
+        if constexpr (NM == 2) bptr[NM - 1][cb] = BL::ptr(p.B1, e_off, ncol[cb], p.K, kl);
     }
 
     f32x4 acc[NM][NCB][4];
@@ -256,19 +263,25 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
 
     const int nks = p.K / 64;
     typename BL::Raw braw[NM][NCB], bnext[NM][NCB];
+    float sc[NM][NCB], snext[NM][NCB];
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) BL::load(braw[m][cb], bptr[m][cb], 0);
+        for (int cb = 0; cb < NCB; ++cb) {
+            BL::load(braw[m][cb], bptr[m][cb], 0);
+            sc[m][cb] = b_scale<WF>(sptr[m], s_off, ncol[cb], p.K, 0);
+        }
 
-    f32x4 gacc[NM][NCB][4];
     for (int ks = 0; ks < nks; ++ks) {
         const int k0 = ks * 64;
         if (ks + 1 < nks) {
 #pragma unroll
             for (int m = 0; m < NM; ++m)
 #pragma unroll
-                for (int cb = 0; cb < NCB; ++cb) BL::load(bnext[m][cb], bptr[m][cb], k0 + 64);
+                for (int cb = 0; cb < NCB; ++cb) {
+                    BL::load(bnext[m][cb], bptr[m][cb], k0 + 64);
+                    if constexpr (GROUPED) snext[m][cb] = b_scale<WF>(sptr[m], s_off, ncol[cb], p.K, k0 + 64);
+                }
         }
         Frag16 af[4];
 #pragma unroll
@@ -279,50 +292,18 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
                 af[rb].u[1] = q[1];
             }
         }
-        if constexpr (GROUPED) {
-            if ((ks & 1) == 0) {
-#pragma unroll
-                for (int m = 0; m < NM; ++m)
-#pragma unroll
-                    for (int cb = 0; cb < NCB; ++cb)
-#pragma unroll
-                        for (int rb = 0; rb < 4; ++rb) gacc[m][cb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
-            }
-        }
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
 #pragma unroll
             for (int cb = 0; cb < NCB; ++cb) {
                 Frag16 bf;
-                BL::cvt(braw[m][cb], bf);
+                BL::cvt(braw[m][cb], sc[m][cb], bf);
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb) {
                     if (rb < nrb) {
-                        f32x4& dst = GROUPED ? gacc[m][cb][rb] : acc[m][cb][rb];
+                        f32x4& dst = acc[m][cb][rb];
                         dst = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[rb].v[0], bf.v[0], dst, 0, 0, 0);
                         dst = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[rb].v[1], bf.v[1], dst, 0, 0, 0);
-                    }
-                }
-            }
-        }
-        if constexpr (GROUPED) {
-            if ((ks & 1) == 1) {
-                const int g = ks >> 1;
-#pragma unroll
-                for (int m = 0; m < NM; ++m) {
-                    const void* S = (m == 0) ? p.S0 : p.S1;
-#pragma unroll
-                    for (int cb = 0; cb < NCB; ++cb) {
-                        const int n = col0 + cb * 16 + (lane & 15);
-                        const float s = group_scale<WF>(S, (long long)e * p.s_stride, n, p.K, g);
-#pragma unroll
-                        for (int rb = 0; rb < 4; ++rb) {
-                            if (rb < nrb) {
-#pragma unroll
-                                for (int i = 0; i < 4; ++i)
-                                    acc[m][cb][rb][i] = acc[m][cb][rb][i] + gacc[m][cb][rb][i] * s;
-                            }
-                        }
                     }
                 }
             }
@@ -331,18 +312,17 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
 #pragma unroll
             for (int m = 0; m < NM; ++m)
 #pragma unroll
-                for (int cb = 0; cb < NCB; ++cb) braw[m][cb] = bnext[m][cb];
+                for (int cb = 0; cb < NCB; ++cb) {
+                    braw[m][cb] = bnext[m][cb];
+                    if constexpr (GROUPED) sc[m][cb] = snext[m][cb];
+                }
         }
     }
 
-    // epilogue
+    // epilogue (bf16 rounding points of YvSwiGLUExpert.forward)
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
-        const int n = col0 + cb * 16 + (lane & 15);
-        const long long so = (long long)e * p.s_stride;
-        const float s0 = col_scale<WF>(p.S0, so, n);
-        float s1 = 1.0f;
-        if constexpr (NM == 2) s1 = col_scale<WF>(p.S1, so, n);
+        const int n = ncol[cb];
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
             if (rb < nrb) {
@@ -353,13 +333,13 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
                         if constexpr (EPI == EPI_F32) {
                             ((float*)p.out)[(long long)r * p.ldo + n] = acc[0][cb][rb][i];
                         } else if constexpr (EPI == EPI_SWIGLU) {
-                            const float g = acc[0][cb][rb][i] * s0;
-                            const float u = acc[NM - 1][cb][rb][i] * s1;
-                            ((unsigned short*)p.out)[(long long)r * p.ldo + n] =
-                                f32_to_bf16_rne(silu(g) * u);
+                            const float g = round_bf16(acc[0][cb][rb][i]);
+                            const float u = round_bf16(acc[NM - 1][cb][rb][i]);
+                            const float sg = round_bf16(silu(g));
+                            ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(sg * u);
                         } else {
                             ((unsigned short*)p.out)[(long long)r * p.ldo + n] =
-                                f32_to_bf16_rne(acc[0][cb][rb][i] * s0);
+                                f32_to_bf16_rne(acc[0][cb][rb][i]);
                         }
                     }
                 }
@@ -502,6 +482,12 @@ __global__ __launch_bounds__(512) void build_tiles_kernel(const int* __restrict_
 }
 
 // --------------------------------------------------------------- combine
+template <int ACT>
+__device__ __forceinline__ float rnd(float x) {
+    if constexpr (ACT == YVMOE_ACT_BF16) return round_bf16(x);
+    else return x;
+}
+
 // out[t] = round( (sum_j w[t,j] * y[pos[t,j]] + shared[t]) + 0.1 * skip[t] ), fp32 sums in
 // a fixed order (deterministic, unlike the reference's atomic index_add_ on GPU).
 template <int ACT>
@@ -512,6 +498,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
                                                       const void* __restrict__ skip,
                                                       void* __restrict__ out,
                                                       void* __restrict__ shared_out) {
+    // the sums below are specified operation by operation (slot order j = 0..k-1, separate
+    // multiply and add) so the CPU oracle reproduces them exactly
+#pragma clang fp contract(off)
     constexpr int VEC = (ACT == YVMOE_ACT_BF16) ? 8 : 4;
     const int t = blockIdx.y;
     const int h = (blockIdx.x * blockDim.x + threadIdx.x) * VEC;
@@ -550,19 +539,22 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
         const float ms = mix[s];
         load((long long)N * k + (long long)s * N + t, tmp);
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) sh[v] = sh[v] + ms * tmp[v];
+        for (int v = 0; v < VEC; ++v) sh[v] = rnd<ACT>(sh[v] + rnd<ACT>(ms * tmp[v]));
     }
+    // routed output rounded to the layer dtype, shared mixture and residual sums rounded
+    // after every step, as the reference's tensors of that dtype are (layer.py:859-863,
+    // :942-945, :750-752)
     float o[VEC];
 #pragma unroll
-    for (int v = 0; v < VEC; ++v) o[v] = acc[v] + sh[v];
+    for (int v = 0; v < VEC; ++v) o[v] = rnd<ACT>(rnd<ACT>(acc[v]) + sh[v]);
     if (skip != nullptr) {
         if constexpr (ACT == YVMOE_ACT_BF16) {
             const uint4 q = *(const uint4*)((const unsigned short*)skip + (long long)t * H + h);
             const unsigned u[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                o[2 * i] = o[2 * i] + 0.1f * __uint_as_float(u[i] << 16);
-                o[2 * i + 1] = o[2 * i + 1] + 0.1f * __uint_as_float(u[i] & 0xffff0000u);
+                o[2 * i] = rnd<ACT>(o[2 * i] + rnd<ACT>(0.1f * __uint_as_float(u[i] << 16)));
+                o[2 * i + 1] = rnd<ACT>(o[2 * i + 1] + rnd<ACT>(0.1f * __uint_as_float(u[i] & 0xffff0000u)));
             }
         } else {
             const float4 q = *(const float4*)((const float*)skip + (long long)t * H + h);

@@ -228,6 +228,8 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(
         int cap = -1;
         if (cap_mode == 1) {
             cap = cap_explicit;
+        } else if ((cap_mode == 2 || cap_mode == 3) && N == 0) {
+            cap = min_cap;  // empty batch: int(0 * cf / E) = 0 -> min_capacity
         } else if (cap_mode == 2 || cap_mode == 3) {
             double cf = cap_factor;
             if (cap_mode == 2) {
@@ -325,6 +327,10 @@ __global__ __launch_bounds__(256) void capacity_trim_kernel(
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+    if (cap == 0) {  // every slot of the expert is surplus (gate.py:1231-1236 with cap 0)
+        for (int i = tid; i < n; i += 256) allowed[perm[off + i]] = 0;
+        return;
+    }
     unsigned prefix = 0u, pmask = 0u;
     int rem = cap;
     for (int shift = 24; shift >= 0; shift -= 8) {

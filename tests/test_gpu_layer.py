@@ -5,6 +5,13 @@ expert count otherwise) the GPU gate logits are checked against float64, the dev
 capacity against the oracle's, the routing bit for bit given the GPU's fp32 logits, and
 the outputs against the oracle's reference forward: bf16 max-abs <= 2e-2 and cosine >=
 0.9999; fp32 max-abs <= 1e-4 and cosine >= 0.999999.
+
+bf16 tolerance: every element within max(2e-2, two bf16 ulps of the reference value), at
+most 1e-5 of the elements beyond 2e-2, cosine >= 0.9999; the raw max-abs is printed. Above
+|out| = 2 a bf16 ulp is 0.0156 (0.031 above 4), and the reference's own bf16 chain moves by up
+to 0.031 max-abs when only the fp32 summation order of its GEMMs changes (CPU measurement at
+cfg4: K summed in two halves vs one pass, 3 of 1.97M elements above 2e-2), so 2e-2 cannot
+bind every element of two correct implementations.
 """
 import numpy as np
 import pytest
@@ -57,16 +64,36 @@ def _run_and_check(oracle, w, skip=None, tokens=None):
     want = o["out"]
     if tokens is not None:
         got, want = got[tokens], want[tokens]
-    tol_abs, tol_cos = _tol(x.dtype)
-    ma, cs = max_abs(got, want), cosine(got, want)
-    print(f"  out max_abs={ma:.3e} cos={cs:.7f}", flush=True)
-    assert ma <= tol_abs and cs >= tol_cos
+    ma, cs, ex = _check_close(got, want)
+    print(f"  out max_abs={ma:.3e} cos={cs:.7f} over-tolerance={ex}", flush=True)
     if spec.num_shared > 0:
         gs, ws = shared.cpu(), o["shared"]
         if tokens is not None:
             gs, ws = gs[tokens], ws[tokens]
-        assert max_abs(gs, ws) <= tol_abs and cosine(gs, ws) >= tol_cos
+        _check_close(gs, ws)
     return out, shared, routing
+
+
+def bf16_ulp(v: torch.Tensor) -> torch.Tensor:
+    """Spacing of bf16 numbers at |v| (2^(floor(log2|v|) - 7))."""
+    a = v.double().abs().clamp(min=2.0 ** -126)
+    return torch.exp2(torch.floor(torch.log2(a)) - 7)
+
+
+def _check_close(got: torch.Tensor, want: torch.Tensor):
+    tol_abs, tol_cos = _tol(want.dtype)
+    d = (got.double() - want.double()).abs()
+    if want.dtype == torch.bfloat16:
+        bound = torch.maximum(torch.full_like(d, tol_abs), 2 * bf16_ulp(want))
+    else:
+        bound = torch.full_like(d, tol_abs)
+    beyond = int((d > bound).sum())
+    over = int((d > tol_abs).sum())
+    ma, cs = float(d.max()), cosine(got, want)
+    assert beyond == 0, f"{beyond} elements beyond max(2e-2, 2 ulp); max_abs={ma}"
+    assert over <= 1e-5 * d.numel(), f"{over} elements above {tol_abs}; max_abs={ma}"
+    assert cs >= tol_cos, cs
+    return ma, cs, over
 
 
 @pytest.mark.parametrize("name,kw", [
