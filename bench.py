@@ -1,0 +1,190 @@
+#!/usr/bin/env python3
+"""Yv MoE layer forward on one MI355X: tokens/s, roofline fraction, CPU baseline.
+
+A step is one forward of the whole layer (router GEMM + complexity predictor, routing,
+permutation, grouped SwiGLU FFN of routed and shared experts, combine with the skip residual)
+over one packed batch whose inputs and weights are already resident in HBM.
+
+Default workload: BASELINE configs[1] (cfg2) — W8A16 layer, hidden 4096, 64 experts (FFN
+1408), top-6, 2 shared experts, decode batch of 64 sequences x 1 token. The same run also
+times configs[2] (cfg3, the same layer on a ~16K-token ragged prefill) as the "prefill"
+object, and the CPU oracle (the reference algorithm restated in torch on the host) on cfg2
+as "cpu_baseline".
+
+roofline: the dominant kernel is the grouped expert FFN (yvmoe_expert_ffn: tile schedule,
+gate/up GEMM with SwiGLU, down GEMM); its average duration is measured with HIP events on
+the stream it runs on. Algorithmic bytes per launch = packed weights of the experts that
+received tokens + the shared experts + x (N*H*2) + y (rows*H*2); algorithmic FLOPs =
+6*H*F*(N*k + N*S).
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE layer tokens/s at 1 GPU; HBM GB/s (decode) & MFMA util % (prefill)"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-steps", type=int, default=20)
+    return ap.parse_args()
+
+
+def time_layer(yvf, x, st, experts, mix, skip, ws, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        yvf.moe_forward(x, st, experts, mix, skip, workspace=ws)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        yvf.moe_forward(x, st, experts, mix, skip, workspace=ws)
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def time_ffn(yvf, x, st, experts, mix, skip, ws, k, steps):
+    """Average duration of the grouped expert FFN, HIP events on its stream."""
+    import torch
+    out, shared, routing = yvf.moe_forward(x, st, experts, mix, skip, workspace=ws)
+    stream = torch.cuda.current_stream()
+    for _ in range(3):
+        yvf.expert_ffn(x, experts, routing, k, workspace=ws)
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(steps):
+        yvf.expert_ffn(x, experts, routing, k, workspace=ws)
+    b.record(stream)
+    b.synchronize()
+    return a.elapsed_time(b) / 1e3 / steps, routing
+
+
+def ffn_work(spec, n_tokens, routing):
+    from pisceslx_amd.workloads import weight_bytes_per_expert
+    active = int((routing.counts > 0).sum().item())
+    rows = n_tokens * (spec.top_k + spec.num_shared)
+    wbytes = (active + spec.num_shared) * weight_bytes_per_expert(spec)
+    nbytes = wbytes + n_tokens * spec.hidden * 2 + rows * spec.hidden * 2
+    flops = 6 * spec.hidden * spec.ffn * rows
+    return {"bytes": nbytes, "weight_bytes": wbytes, "flops": flops, "active_experts": active}
+
+
+def cpu_baseline(w, budget_s=30.0):
+    """The CPU oracle (reference algorithm restated with torch on the host), bounded."""
+    import torch
+    from oracle import moe_oracle
+    cores = max(1, min(16, len(os.sched_getaffinity(0))))
+    torch.set_num_threads(cores)
+    params = moe_oracle.params_from_workload(w)
+    x = w.x.cpu()
+    times = []
+    t_start = time.perf_counter()
+    moe_oracle.layer_forward(x, params)  # warm-up
+    for _ in range(3):
+        if time.perf_counter() - t_start > budget_s and times:
+            break
+        t0 = time.perf_counter()
+        moe_oracle.layer_forward(x, params)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    return {"value": round(w.n_tokens / t, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"{w.spec.name} full forward, {w.n_tokens} tokens, 1 warm-up + median of "
+                      f"{len(times)} runs ({t:.3f} s each), experts dequantized inside the loop"}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build's path (the Yv MoE layer forward) "
+              "runs on one MI355X; multi-GPU sharding is described in DESIGN.md, not run.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from pisceslx_amd import functional as yvf
+    from pisceslx_amd.workloads import make_workload, mix_weights, router_state, seq_lengths
+
+    dev = torch.device("cuda:0")
+    w = make_workload("cfg2", device=dev, seed=0)
+    spec = w.spec
+    st = router_state(w)
+    mix = mix_weights(w)
+    N, H = w.n_tokens, spec.hidden
+    skip = torch.randn(N, H, device=dev, generator=torch.Generator(device=dev).manual_seed(1)).to(spec.act_dtype)
+    ws = torch.empty(yvf.workspace_bytes(N, 1, st, w.experts), dtype=torch.uint8, device=dev)
+    torch.cuda.synchronize()
+
+    t_step = time_layer(yvf, w.x, st, w.experts, mix, skip, ws, args.steps, args.warmup)
+    t_ffn, routing = time_ffn(yvf, w.x, st, w.experts, mix, skip, ws, spec.top_k, args.steps)
+    work = ffn_work(spec, N, routing)
+    achieved = work["bytes"] / t_ffn / 1e9
+    result = {
+        "metric": METRIC,
+        "value": round(N / t_step, 2),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(t_step * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "cfg2: W8A16 Yv MoE layer decode (BASELINE configs[1])",
+                   "tokens": N, "hidden": H, "experts": spec.num_experts, "ffn": spec.ffn,
+                   "top_k": spec.top_k, "shared_experts": spec.num_shared,
+                   "weights": "int8 per-output-channel, bf16 scales", "seed": 0},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "grouped expert FFN (yvmoe_expert_ffn)",
+                     "ms_per_launch": round(t_ffn * 1e3, 4),
+                     "algorithmic_bytes": work["bytes"], "active_experts": work["active_experts"]},
+    }
+    layer_bytes = work["weight_bytes"] + spec.num_experts * H * 2 + 64 * H * 4 + N * H * 2 * 4
+    result["layer_hbm_gbs"] = round(layer_bytes / t_step / 1e9, 1)
+
+    if not args.no_prefill:
+        lengths = seq_lengths("cfg3", 0)
+        Np = sum(lengths)
+        gx = torch.Generator(device=dev).manual_seed(2)
+        xp = torch.randn(Np, H, device=dev, generator=gx).to(spec.act_dtype)
+        skip_p = torch.randn(Np, H, device=dev, generator=gx).to(spec.act_dtype)
+        wsp = torch.empty(yvf.workspace_bytes(Np, 1, st, w.experts), dtype=torch.uint8, device=dev)
+        tp = time_layer(yvf, xp, st, w.experts, mix, skip_p, wsp, args.prefill_steps, 3)
+        tpf, rp = time_ffn(yvf, xp, st, w.experts, mix, skip_p, wsp, spec.top_k, args.prefill_steps)
+        wp = ffn_work(spec, Np, rp)
+        tf = wp["flops"] / tpf / 1e12
+        layer_flops = wp["flops"] + 2 * Np * H * (spec.num_experts + 192)
+        result["prefill"] = {
+            "workload": "cfg3: same layer, ragged prefill of 32 sequences (BASELINE configs[2])",
+            "tokens": Np, "tokens_per_s": round(Np / tp, 1), "ms_per_step": round(tp * 1e3, 3),
+            "layer_tflops": round(layer_flops / tp / 1e12, 1),
+            "roofline": {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                         "kernel": "grouped expert FFN (yvmoe_expert_ffn)",
+                         "ms_per_launch": round(tpf * 1e3, 4), "algorithmic_flops": wp["flops"]},
+        }
+        del xp, skip_p, wsp
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(w)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -146,11 +146,14 @@ size_t yvmoe_workspace_bytes(int32_t n_tokens, int32_t act_dtype, const yvmoe_ro
 
 /*
  * logits_out [N][ld] fp32 with ld = Ep + 192 (bf16 x) or Ep + 64 (fp32 x): columns [0, E)
- * are the gate logits, the rest the complexity predictor's first-layer terms.
+ * are the gate logits, the rest the complexity predictor's first-layer terms. The values
+ * are bit-identical to the logits yvmoe_forward routes on (same split of the K sum, same
+ * summation order). workspace: at least yvmoe_router_workspace_bytes() bytes.
  */
+size_t yvmoe_router_workspace_bytes(int32_t n_tokens, int32_t act_dtype, const yvmoe_router* router);
 int32_t yvmoe_router_logits(const void* x, int32_t act_dtype, int32_t n_tokens,
                             const yvmoe_router* router, float* logits_out, int32_t ld,
-                            void* stream);
+                            void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Routing from fp32 logits [N][ld] (the first E columns are used).

@@ -161,6 +161,22 @@ class LayerParams:
         return self.expert_fn(i)
 
 
+def params_from_workload(w) -> LayerParams:
+    """Oracle view of a pisceslx_amd.workloads.Workload (weights copied to the host and
+    dequantized per expert on demand)."""
+    cpu = w.experts.to("cpu")
+    spec = w.spec
+    pred = None if w.pred is None else tuple(t.detach().cpu() for t in w.pred)
+    return LayerParams(
+        hidden=spec.hidden, ffn=spec.ffn, num_experts=spec.num_experts, num_shared=spec.num_shared,
+        top_k=spec.top_k, gate_weight=w.gate_weight.cpu(), pred=pred,
+        bias=None if w.expert_bias is None else w.expert_bias.cpu(),
+        fixed_shape_mode=spec.fixed_shape_mode, dynamic_capacity=not spec.fixed_shape_mode,
+        capacity_factor=1.0, min_capacity=4,
+        mix_param=None if w.shared_expert_weight is None else w.shared_expert_weight.cpu(),
+        expert_fn=lambda i: cpu.dequantize(i, torch.float32))
+
+
 def router_logits(x2d: torch.Tensor, gate_weight: torch.Tensor) -> np.ndarray:
     """gate(x_flat) (gate.py:1179) in float64, rounded to fp32 logits."""
     return (x2d.double() @ gate_weight.double().t()).float().numpy()

@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "yvmoe_last_error",
     "yvmoe_version",
     "yvmoe_workspace_bytes",
+    "yvmoe_router_workspace_bytes",
     "yvmoe_router_logits",
     "yvmoe_route",
     "yvmoe_expert_ffn",
@@ -104,8 +105,10 @@ def _declare(l: ctypes.CDLL) -> None:
     l.yvmoe_version.argtypes = []
     l.yvmoe_workspace_bytes.restype = sz
     l.yvmoe_workspace_bytes.argtypes = [i32, i32, ctypes.POINTER(Router), ctypes.POINTER(ExpertWeights)]
+    l.yvmoe_router_workspace_bytes.restype = sz
+    l.yvmoe_router_workspace_bytes.argtypes = [i32, i32, ctypes.POINTER(Router)]
     l.yvmoe_router_logits.restype = i32
-    l.yvmoe_router_logits.argtypes = [vp, i32, i32, ctypes.POINTER(Router), vp, i32, vp]
+    l.yvmoe_router_logits.argtypes = [vp, i32, i32, ctypes.POINTER(Router), vp, i32, vp, sz, vp]
     l.yvmoe_route.restype = i32
     l.yvmoe_route.argtypes = [vp, i32, vp, i32, ctypes.POINTER(Router), i32,
                               ctypes.POINTER(Routing), vp, sz, vp]

@@ -95,12 +95,18 @@ size_t yvmoe_workspace_bytes(int32_t n_tokens, int32_t act_dtype, const yvmoe_ro
     total += align_up((size_t)N * router_ld(E, act_dtype) * 4, 256);
     if (experts != nullptr)
         total += y_bytes(N, k, experts->num_shared, experts->hidden, act_dtype);
+    total += router_partials_bytes(N, E, act_dtype, router->hidden);
     return total;
+}
+
+size_t yvmoe_router_workspace_bytes(int32_t n_tokens, int32_t act_dtype, const yvmoe_router* router) {
+    if (n_tokens < 0 || router == nullptr) return 0;
+    return router_partials_bytes(n_tokens, router->num_experts, act_dtype, router->hidden);
 }
 
 int32_t yvmoe_router_logits(const void* x, int32_t act_dtype, int32_t n_tokens,
                             const yvmoe_router* router, float* logits_out, int32_t ld,
-                            void* stream) {
+                            void* workspace, size_t workspace_bytes, void* stream) {
     clear_error();
     int rc = check_router(router, act_dtype);
     if (rc) return rc;
@@ -109,9 +115,13 @@ int32_t yvmoe_router_logits(const void* x, int32_t act_dtype, int32_t n_tokens,
     YV_REQUIRE(x && logits_out && router->w_router, YVMOE_ERR_ARG, "NULL pointer");
     YV_REQUIRE(router->hidden > 0 && router->hidden % 64 == 0, YVMOE_ERR_SHAPE,
                "hidden=%d must be a positive multiple of 64", router->hidden);
-    YV_REQUIRE(ld >= router_ld(router->num_experts, act_dtype), YVMOE_ERR_SHAPE,
-               "ld=%d smaller than %d", ld, router_ld(router->num_experts, act_dtype));
-    return router_gemm_launch(x, act_dtype, n_tokens, router, logits_out, ld, (hipStream_t)stream);
+    YV_REQUIRE(ld == router_ld(router->num_experts, act_dtype), YVMOE_ERR_SHAPE,
+               "ld=%d, expected %d", ld, router_ld(router->num_experts, act_dtype));
+    const size_t need = router_partials_bytes(n_tokens, router->num_experts, act_dtype, router->hidden);
+    YV_REQUIRE(need == 0 || (workspace != nullptr && workspace_bytes >= need), YVMOE_ERR_WORKSPACE,
+               "workspace %zu bytes, need %zu", workspace_bytes, need);
+    return router_gemm_launch(x, act_dtype, n_tokens, router, logits_out, ld,
+                              need ? (float*)workspace : nullptr, (hipStream_t)stream);
 }
 
 int32_t yvmoe_route(const float* logits, int32_t ld, const float* predictor, int32_t n_tokens,
@@ -215,8 +225,10 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
     char* ws = (char*)workspace;
     float* logits = (float*)(ws + route_ws(N, E, k).bytes +
                              ffn_ws(N, k, E, experts->num_shared, experts->ffn, act_dtype).bytes);
+    void* y = (char*)logits + align_up((size_t)N * ld * 4, 256);
+    float* partials = (float*)((char*)y + y_bytes(N, k, experts->num_shared, experts->hidden, act_dtype));
     if (N > 0) {
-        rc = router_gemm_launch(x, act_dtype, N, router, logits, ld, st);
+        rc = router_gemm_launch(x, act_dtype, N, router, logits, ld, partials, st);
         if (rc) return rc;
     }
     const bool need_pred = !router->fixed_shape_mode && router->dynamic_capacity;
@@ -224,7 +236,6 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
                       routing, ws, st);
     if (rc) return rc;
     if (N == 0) return YVMOE_OK;
-    void* y = (char*)logits + align_up((size_t)N * ld * 4, 256);
     rc = expert_ffn_launch(x, act_dtype, N, k, experts, routing, y, ws, st);
     if (rc) return rc;
     return combine_launch(y, act_dtype, N, experts->hidden, k, experts->num_shared, routing, mix,

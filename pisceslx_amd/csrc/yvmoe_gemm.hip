@@ -57,6 +57,8 @@ struct GemmParams {
     const int* ntiles;
     const int* seg_start;
     int nrows;  // rows when there is no tile table
+    int kchunk;              // K range of one split (multiple of 64); K when not split
+    long long split_stride;  // output elements between splits (EPI_F32 partial sums)
 };
 
 // Round-to-nearest-even fp32 -> bf16 pair (v_cvt_pk_bf16_f32), lo in bits 0..15.
@@ -214,6 +216,7 @@ template <int WF, int EPI, int NCB>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
     constexpr int NM = NMat<EPI>::value;
     constexpr bool GROUPED = (WF == YVMOE_W_INT4 || WF == YVMOE_W_FP8);
+    constexpr int R = 3;  // B ring: loads run R-1 k-steps ahead of the MFMAs
     typedef BLoad<WF> BL;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -233,13 +236,15 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
     if (col0 >= p.ncols) return;
     const int nrb = min(4, (seg_end - row0 + 15) / 16);
     const int kl = (lane >> 4) * 16;  // this lane's k offset inside a 64-wide k-step
+    const int kbeg = blockIdx.z * p.kchunk;
+    const int nks = (min(p.K, kbeg + p.kchunk) - kbeg) / 64;
 
     const char* arow[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
         int r = row0 + rb * 16 + (lane & 15);
         if (r >= seg_end) r = row0;
-        arow[rb] = (const char*)p.A + ((long long)map_row(p, r) * p.lda + kl) * 2;
+        arow[rb] = (const char*)p.A + ((long long)map_row(p, r) * p.lda + kbeg + kl) * 2;
     }
     const long long e_off = (long long)e * p.b_stride;
     const long long s_off = (long long)e * p.s_stride;
@@ -249,8 +254,8 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
         ncol[cb] = col0 + cb * 16 + (lane & 15);
-        bptr[0][cb] = BL::ptr(p.B0, e_off, ncol[cb], p.K, kl);
-        if constexpr (NM == 2) bptr[NM - 1][cb] = BL::ptr(p.B1, e_off, ncol[cb], p.K, kl);
+        bptr[0][cb] = BL::ptr(p.B0, e_off, ncol[cb], p.K, kbeg + kl);
+        if constexpr (NM == 2) bptr[NM - 1][cb] = BL::ptr(p.B1, e_off, ncol[cb], p.K, kbeg + kl);
     }
 
     f32x4 acc[NM][NCB][4];
@@ -261,43 +266,39 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) acc[m][cb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int nks = p.K / 64;
-    typename BL::Raw braw[NM][NCB], bnext[NM][NCB];
-    float sc[NM][NCB], snext[NM][NCB];
+    typename BL::Raw braw[R][NM][NCB];
+    float sc[R][NM][NCB];
+    auto load_b = [&](int slot_ks, typename BL::Raw (&dst)[NM][NCB], float (&sdst)[NM][NCB]) {
+        const int k0 = slot_ks * 64;
 #pragma unroll
-    for (int m = 0; m < NM; ++m)
+        for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int cb = 0; cb < NCB; ++cb) {
-            BL::load(braw[m][cb], bptr[m][cb], 0);
-            sc[m][cb] = b_scale<WF>(sptr[m], s_off, ncol[cb], p.K, 0);
-        }
-
-    for (int ks = 0; ks < nks; ++ks) {
-        const int k0 = ks * 64;
-        if (ks + 1 < nks) {
-#pragma unroll
-            for (int m = 0; m < NM; ++m)
-#pragma unroll
-                for (int cb = 0; cb < NCB; ++cb) {
-                    BL::load(bnext[m][cb], bptr[m][cb], k0 + 64);
-                    if constexpr (GROUPED) snext[m][cb] = b_scale<WF>(sptr[m], s_off, ncol[cb], p.K, k0 + 64);
-                }
-        }
-        Frag16 af[4];
+            for (int cb = 0; cb < NCB; ++cb) {
+                BL::load(dst[m][cb], bptr[m][cb], k0);
+                if constexpr (GROUPED)
+                    sdst[m][cb] = b_scale<WF>(sptr[m], s_off, ncol[cb], p.K, kbeg + k0);
+                else
+                    sdst[m][cb] = b_scale<WF>(sptr[m], s_off, ncol[cb], p.K, 0);
+            }
+    };
+    auto load_a = [&](int ks, Frag16 (&af)[4]) {
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
             if (rb < nrb) {
-                const uint4* q = (const uint4*)(arow[rb] + (size_t)k0 * 2);
+                const uint4* q = (const uint4*)(arow[rb] + (size_t)ks * 128);
                 af[rb].u[0] = q[0];
                 af[rb].u[1] = q[1];
             }
         }
+    };
+    auto mma = [&](const typename BL::Raw (&bw)[NM][NCB], const float (&bs)[NM][NCB],
+                   const Frag16 (&af)[4]) {
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
 #pragma unroll
             for (int cb = 0; cb < NCB; ++cb) {
                 Frag16 bf;
-                BL::cvt(braw[m][cb], sc[m][cb], bf);
+                BL::cvt(bw[m][cb], bs[m][cb], bf);
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb) {
                     if (rb < nrb) {
@@ -308,14 +309,24 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
                 }
             }
         }
-        if (ks + 1 < nks) {
+    };
+
 #pragma unroll
-            for (int m = 0; m < NM; ++m)
+    for (int r = 0; r < R - 1; ++r)
+        if (r < nks) load_b(r, braw[r], sc[r]);
+    Frag16 acur[4], anext[4];
+    if (nks > 0) load_a(0, acur);
+    for (int ks0 = 0; ks0 < nks; ks0 += R) {
 #pragma unroll
-                for (int cb = 0; cb < NCB; ++cb) {
-                    braw[m][cb] = bnext[m][cb];
-                    if constexpr (GROUPED) sc[m][cb] = snext[m][cb];
-                }
+        for (int r = 0; r < R; ++r) {
+            const int ks = ks0 + r;
+            if (ks < nks) {
+                if (ks + R - 1 < nks) load_b(ks + R - 1, braw[(r + R - 1) % R], sc[(r + R - 1) % R]);
+                if (ks + 1 < nks) load_a(ks + 1, anext);
+                mma(braw[r], sc[r], acur);
+#pragma unroll
+                for (int rb = 0; rb < 4; ++rb) acur[rb] = anext[rb];
+            }
         }
     }
 
@@ -331,7 +342,8 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
                     const int r = row0 + rb * 16 + (lane >> 4) * 4 + i;
                     if (r < seg_end) {
                         if constexpr (EPI == EPI_F32) {
-                            ((float*)p.out)[(long long)r * p.ldo + n] = acc[0][cb][rb][i];
+                            ((float*)p.out)[blockIdx.z * p.split_stride + (long long)r * p.ldo + n] =
+                                acc[0][cb][rb][i];
                         } else if constexpr (EPI == EPI_SWIGLU) {
                             const float g = round_bf16(acc[0][cb][rb][i]);
                             const float u = round_bf16(acc[NM - 1][cb][rb][i]);
@@ -371,6 +383,8 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
     if (col0 >= p.ncols) return;
     const int nrb = min(4, (seg_end - row0 + 15) / 16);
     const int kl = (lane >> 4) * 4;
+    const int kbeg = blockIdx.z * p.kchunk;
+    const int kend = min(p.K, kbeg + p.kchunk);
     const float* arow[4];
 #pragma unroll
     for (int rb = 0; rb < 4; ++rb) {
@@ -393,7 +407,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
         for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
             for (int rb = 0; rb < 4; ++rb) acc[m][cb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    for (int k0 = 0; k0 < p.K; k0 += 16) {
+    for (int k0 = kbeg; k0 < kend; k0 += 16) {
         float4 bv[NM][NCB];
 #pragma unroll
         for (int m = 0; m < NM; ++m)
@@ -431,7 +445,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
                         float v;
                         if constexpr (EPI == EPI_SWIGLU) v = silu(acc[0][cb][rb][i]) * acc[NM - 1][cb][rb][i];
                         else v = acc[0][cb][rb][i];
-                        ((float*)p.out)[(long long)r * p.ldo + n] = v;
+                        ((float*)p.out)[blockIdx.z * p.split_stride + (long long)r * p.ldo + n] = v;
                     }
                 }
             }
@@ -581,14 +595,28 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
     }
 }
 
-// Picks NCB so that every wavefront's columns are in range, and launches.
+// Sums split-K partial results in split order (deterministic): out[i] = sum_z part[z][i].
+__global__ __launch_bounds__(256) void reduce_splits_kernel(const float* __restrict__ part, int nsplit,
+                                                            long long stride, long long n,
+                                                            float* __restrict__ out) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    float s = part[i];
+    for (int z = 1; z < nsplit; ++z) s = s + part[(long long)z * stride + i];
+    out[i] = s;
+}
+
+// Launches one GEMM: grid (tiles, column groups, K splits); NCB 16-column blocks per wave.
 template <int EPI>
-int gemm_dispatch(int act, int wf, GemmParams p, int ntiles_max, hipStream_t st,
-                  const char* name) {
-    const int ncb = (p.ncols % 32 == 0) ? 2 : 1;
-    const int cols_per_wg = 4 * ncb * 16;
-    dim3 grid(ntiles_max, (p.ncols + cols_per_wg - 1) / cols_per_wg);
+int gemm_dispatch(int act, int wf, GemmParams p, int ntiles_max, int ncb, int ksplit,
+                  hipStream_t st, const char* name) {
     if (ntiles_max <= 0) return YVMOE_OK;
+    if (p.ncols % (16 * ncb) != 0) {
+        set_error("%s: %d columns are not a multiple of %d", name, p.ncols, 16 * ncb);
+        return YVMOE_ERR_SHAPE;
+    }
+    const int cols_per_wg = 4 * ncb * 16;
+    dim3 grid(ntiles_max, (p.ncols + cols_per_wg - 1) / cols_per_wg, ksplit);
     if (act == YVMOE_ACT_F32) {
         if (ncb == 2) gemm_f32_kernel<EPI, 2><<<grid, 256, 0, st>>>(p);
         else gemm_f32_kernel<EPI, 1><<<grid, 256, 0, st>>>(p);
@@ -614,7 +642,7 @@ int gemm_dispatch(int act, int wf, GemmParams p, int ntiles_max, hipStream_t st,
 }  // namespace
 
 int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, float* out, int ld,
-                       hipStream_t st) {
+                       float* partials, hipStream_t st) {
     GemmParams p{};
     p.A = x;
     p.lda = r->hidden;
@@ -622,11 +650,25 @@ int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, flo
     p.B0 = r->w_router;
     p.K = r->hidden;
     p.ncols = router_ld(r->num_experts, act);
-    p.out = out;
     p.ldo = ld;
     p.nrows = N;
     const int wf = (act == YVMOE_ACT_F32) ? YVMOE_W_F32 : YVMOE_W_BF16;
-    return gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), st, "router_gemm");
+    const int ks = router_ksplit(N, r->num_experts, act, r->hidden);
+    p.kchunk = r->hidden / ks;
+    if (ks == 1 || partials == nullptr) {
+        p.kchunk = r->hidden;
+        p.out = out;
+        const int ncb = (p.ncols % 32 == 0) ? 2 : 1;
+        return gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), ncb, 1, st, "router_gemm");
+    }
+    p.out = partials;
+    p.split_stride = (long long)N * ld;
+    int rc = gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), 1, ks, st, "router_gemm");
+    if (rc) return rc;
+    const long long n = (long long)N * ld;
+    reduce_splits_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(partials, ks, n, n, out);
+    YV_LAUNCH_CHECK("router_reduce");
+    return YVMOE_OK;
 }
 
 int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_weights* w,
@@ -668,7 +710,8 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.ncols = F;
     p.out = hbuf;
     p.ldo = F;
-    int rc = gemm_dispatch<EPI_SWIGLU>(act, wf, p, T, st, "expert_gemm1");
+    p.kchunk = H;
+    int rc = gemm_dispatch<EPI_SWIGLU>(act, wf, p, T, (F % 32 == 0) ? 2 : 1, 1, st, "expert_gemm1");
     if (rc != YVMOE_OK) return rc;
     // GEMM2: y = h Wd^T (rows already in sorted order)
     p.A = hbuf;
@@ -686,7 +729,8 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.ncols = H;
     p.out = y;
     p.ldo = H;
-    return gemm_dispatch<EPI_DOWN>(act, wf, p, T, st, "expert_gemm2");
+    p.kchunk = F;
+    return gemm_dispatch<EPI_DOWN>(act, wf, p, T, (H % 32 == 0) ? 2 : 1, 1, st, "expert_gemm2");
 }
 
 int combine_launch(const void* y, int act, int N, int H, int k, int S, const yvmoe_routing* routing,

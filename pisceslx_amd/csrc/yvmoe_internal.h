@@ -44,6 +44,21 @@ inline int router_ld(int E, int act) {
     return pad16(E) + (act == YVMOE_ACT_BF16 ? 3 * kPredDim : kPredDim);
 }
 
+// K splits of the router GEMM: enough work-groups to spread a small batch over the chip,
+// at least 128 of K per split (2 k-steps); partial sums are reduced in split order.
+inline int router_ksplit(int N, int E, int act, int H) {
+    const int groups = ceil_div(router_ld(E, act), 64);
+    const int wgs = ceil_div(N > 0 ? N : 1, 64) * groups;
+    int ks = 1;
+    while (wgs * ks * 2 <= 512 && H % (ks * 2 * 64) == 0 && H / (ks * 2) >= 128) ks *= 2;
+    return ks;
+}
+
+inline size_t router_partials_bytes(int N, int E, int act, int H) {
+    const int ks = router_ksplit(N, E, act, H);
+    return ks > 1 ? align_up((size_t)ks * N * router_ld(E, act) * 4, 256) : 0;
+}
+
 // Upper bound on the number of 64-row GEMM tiles over all segments.
 inline int max_tiles(int N, int k, int E, int S) {
     return ceil_div(N * k, kTileRows) + E + S * ceil_div(N, kTileRows);
@@ -102,7 +117,7 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
                  hipStream_t st);
 // GEMMs and combine (yvmoe_gemm.hip)
 int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, float* out,
-                       int ld, hipStream_t st);
+                       int ld, float* partials, hipStream_t st);
 int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_weights* w,
                       const yvmoe_routing* routing, void* y, char* ws, hipStream_t st);
 int combine_launch(const void* y, int act, int N, int H, int k, int S,

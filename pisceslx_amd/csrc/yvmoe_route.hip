@@ -48,9 +48,9 @@ __device__ __forceinline__ bool better(float v1, int e1, float v2, int e2) {
     return v1 > v2 || (v1 == v2 && e1 < e2);
 }
 
-// One block = 64 tokens; 16 lanes per token, 16 tokens per pass, 4 passes.
+// One block = 64 tokens, 16 lanes per token, all 64 tokens in one pass (1024 threads).
 template <int NV>
-__global__ __launch_bounds__(256) void route_topk_kernel(
+__global__ __launch_bounds__(1024) void route_topk_kernel(
     const float* __restrict__ logits, int ld, const float* __restrict__ bias,
     const float* __restrict__ pred, int pred_ld, int pred_terms, const float* __restrict__ b1,
     const float* __restrict__ w2, const float* __restrict__ b2, int N, int E, int k,
@@ -65,8 +65,8 @@ __global__ __launch_bounds__(256) void route_topk_kernel(
     if (tid < kTokPerBlock) score[tid] = 0.0f;
     __syncthreads();
 
-    for (int pass = 0; pass < kTokPerBlock / kLanes; ++pass) {
-        const int tl = pass * kLanes + g;
+    {
+        const int tl = g;
         const int t = blockIdx.x * kTokPerBlock + tl;
         if (t < N) {  // uniform across the 16 lanes of a token
             float z[NV];
@@ -454,7 +454,7 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
         return YVMOE_OK;
     }
 #define YV_TOPK(NVV)                                                                        \
-    route_topk_kernel<NVV><<<nb, 256, 0, st>>>(logits, ld, r->bias, use_pred, pred_ld,       \
+    route_topk_kernel<NVV><<<nb, 1024, 0, st>>>(logits, ld, r->bias, use_pred, pred_ld,      \
                                                 pred_terms, r->b1, r->w2, r->b2, N, E, k,    \
                                                 out->indices, topp, w0, allowed, blockhist, \
                                                 blocksum)

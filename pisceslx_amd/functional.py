@@ -118,8 +118,10 @@ def router_logits(x2d: torch.Tensor, router: RouterState) -> torch.Tensor:
     ld = router_ld(router.num_experts, act)
     out = torch.empty(N, ld, dtype=torch.float32, device=dev)
     r = router.struct()
+    ws = _workspace(int(_lib.lib().yvmoe_router_workspace_bytes(N, act, ctypes.byref(r))), dev)
     _lib.check(_lib.lib().yvmoe_router_logits(x2d.data_ptr(), act, N, ctypes.byref(r),
-                                               out.data_ptr(), ld, _stream(dev)),
+                                               out.data_ptr(), ld, ws.data_ptr(), ws.numel(),
+                                               _stream(dev)),
                "yvmoe_router_logits")
     return out
 
