@@ -24,6 +24,8 @@
 // holds D[row 4*(l/16)+i][col l%16]. Each lane loads 16 consecutive k (bf16 path) or 4
 // (fp32 path); the two (four) MFMAs of a k-step use the same k permutation for A and B,
 // which leaves the sum unchanged.
+#include <algorithm>
+
 #include "yvmoe_internal.h"
 
 namespace yvmoe {
@@ -212,11 +214,14 @@ struct NMat {
 };
 
 // ------------------------------------------------------------------ bf16 activations
-template <int WF, int EPI, int NCB>
+// RB: B-operand ring depth (weight loads run RB-1 k-steps ahead of the MFMAs); RA: A-operand
+// ring depth (RA divides RB).
+template <int WF, int EPI, int NCB, int MAXRB, int RB = 4, int RA = 2>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
     constexpr int NM = NMat<EPI>::value;
     constexpr bool GROUPED = (WF == YVMOE_W_INT4 || WF == YVMOE_W_FP8);
-    constexpr int R = 3;  // B ring: loads run R-1 k-steps ahead of the MFMAs
+    static_assert(RB % RA == 0, "A ring depth must divide the B ring depth");
+    constexpr int R = RB;
     typedef BLoad<WF> BL;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -228,20 +233,20 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
         row0 = p.tile_row0[tile];
         seg_end = p.seg_start[e + 1];
     } else {
-        row0 = blockIdx.x * kTileRows;
+        row0 = blockIdx.x * MAXRB * 16;
         if (row0 >= p.nrows) return;
         seg_end = p.nrows;
     }
     const int col0 = (blockIdx.y * 4 + wave) * NCB * 16;
     if (col0 >= p.ncols) return;
-    const int nrb = min(4, (seg_end - row0 + 15) / 16);
+    const int nrb = min(MAXRB, (seg_end - row0 + 15) / 16);
     const int kl = (lane >> 4) * 16;  // this lane's k offset inside a 64-wide k-step
     const int kbeg = blockIdx.z * p.kchunk;
     const int nks = (min(p.K, kbeg + p.kchunk) - kbeg) / 64;
 
-    const char* arow[4];
+    const char* arow[MAXRB];
 #pragma unroll
-    for (int rb = 0; rb < 4; ++rb) {
+    for (int rb = 0; rb < MAXRB; ++rb) {
         int r = row0 + rb * 16 + (lane & 15);
         if (r >= seg_end) r = row0;
         arow[rb] = (const char*)p.A + ((long long)map_row(p, r) * p.lda + kbeg + kl) * 2;
@@ -258,16 +263,23 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
         if constexpr (NM == 2) bptr[NM - 1][cb] = BL::ptr(p.B1, e_off, ncol[cb], p.K, kbeg + kl);
     }
 
-    f32x4 acc[NM][NCB][4];
+    f32x4 acc[NM][NCB][MAXRB];
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
         for (int cb = 0; cb < NCB; ++cb)
 #pragma unroll
-            for (int rb = 0; rb < 4; ++rb) acc[m][cb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+            for (int rb = 0; rb < MAXRB; ++rb) acc[m][cb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     typename BL::Raw braw[R][NM][NCB];
-    float sc[R][NM][NCB];
+    // per-k-step scales for group-scaled formats (ring), one scale per column otherwise
+    float sc[GROUPED ? R : 1][NM][NCB];
+    if constexpr (!GROUPED) {
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int cb = 0; cb < NCB; ++cb) sc[0][m][cb] = b_scale<WF>(sptr[m], s_off, ncol[cb], p.K, 0);
+    }
     auto load_b = [&](int slot_ks, typename BL::Raw (&dst)[NM][NCB], float (&sdst)[NM][NCB]) {
         const int k0 = slot_ks * 64;
 #pragma unroll
@@ -277,22 +289,21 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
                 BL::load(dst[m][cb], bptr[m][cb], k0);
                 if constexpr (GROUPED)
                     sdst[m][cb] = b_scale<WF>(sptr[m], s_off, ncol[cb], p.K, kbeg + k0);
-                else
-                    sdst[m][cb] = b_scale<WF>(sptr[m], s_off, ncol[cb], p.K, 0);
             }
     };
-    auto load_a = [&](int ks, Frag16 (&af)[4]) {
+    // Loads are unconditional (k-step clamped to the last one, row blocks past nrb read the
+    // tile's first row): with no branch around them the compiler can wait for exactly the
+    // oldest in-flight load instead of draining the whole ring before every MFMA.
+    auto load_a = [&](int ks, Frag16 (&af)[MAXRB]) {
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
-            if (rb < nrb) {
-                const uint4* q = (const uint4*)(arow[rb] + (size_t)ks * 128);
-                af[rb].u[0] = q[0];
-                af[rb].u[1] = q[1];
-            }
+        for (int rb = 0; rb < MAXRB; ++rb) {
+            const uint4* q = (const uint4*)(arow[rb] + (size_t)ks * 128);
+            af[rb].u[0] = q[0];
+            af[rb].u[1] = q[1];
         }
     };
     auto mma = [&](const typename BL::Raw (&bw)[NM][NCB], const float (&bs)[NM][NCB],
-                   const Frag16 (&af)[4]) {
+                   const Frag16 (&af)[MAXRB]) {
 #pragma unroll
         for (int m = 0; m < NM; ++m) {
 #pragma unroll
@@ -300,7 +311,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
                 Frag16 bf;
                 BL::cvt(bw[m][cb], bs[m][cb], bf);
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb) {
+                for (int rb = 0; rb < MAXRB; ++rb) {
                     if (rb < nrb) {
                         f32x4& dst = acc[m][cb][rb];
                         dst = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[rb].v[0], bf.v[0], dst, 0, 0, 0);
@@ -310,23 +321,32 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
             }
         }
     };
+    auto kc = [&](int ks) { return ks < nks ? ks : nks - 1; };
 
+    constexpr int SR = GROUPED ? R : 1;
+    Frag16 abuf[RA][MAXRB];
+    if (nks > 0) {
 #pragma unroll
-    for (int r = 0; r < R - 1; ++r)
-        if (r < nks) load_b(r, braw[r], sc[r]);
-    Frag16 acur[4], anext[4];
-    if (nks > 0) load_a(0, acur);
-    for (int ks0 = 0; ks0 < nks; ks0 += R) {
+        for (int r = 0; r < RB - 1; ++r) load_b(kc(r), braw[r], sc[r % SR]);
 #pragma unroll
-        for (int r = 0; r < R; ++r) {
+        for (int r = 0; r < RA - 1; ++r) load_a(kc(r), abuf[r]);
+    }
+    int ks0 = 0;
+    for (; ks0 + RB <= nks; ks0 += RB) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
             const int ks = ks0 + r;
-            if (ks < nks) {
-                if (ks + R - 1 < nks) load_b(ks + R - 1, braw[(r + R - 1) % R], sc[(r + R - 1) % R]);
-                if (ks + 1 < nks) load_a(ks + 1, anext);
-                mma(braw[r], sc[r], acur);
+            load_b(kc(ks + RB - 1), braw[(r + RB - 1) % RB], sc[((r + RB - 1) % RB) % SR]);
+            load_a(kc(ks + RA - 1), abuf[(r + RA - 1) % RA]);
+            mma(braw[r], sc[r % SR], abuf[r % RA]);
+        }
+    }
+    // tail (fewer than RB steps): their weights are already in ring slots 0..nks-ks0-1
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb) acur[rb] = anext[rb];
-            }
+    for (int r = 0; r < RB - 1; ++r) {
+        if (ks0 + r < nks) {
+            load_a(kc(ks0 + r + RA - 1), abuf[(r + RA - 1) % RA]);
+            mma(braw[r], sc[r % SR], abuf[r % RA]);
         }
     }
 
@@ -335,7 +355,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
     for (int cb = 0; cb < NCB; ++cb) {
         const int n = ncol[cb];
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) {
+        for (int rb = 0; rb < MAXRB; ++rb) {
             if (rb < nrb) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
@@ -358,6 +378,179 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
             }
         }
     }
+}
+
+// ------------------------------------------------------------------ bf16, streaming form
+// Weight-streaming form for batches whose experts hold few rows (decode). A work-group of 4
+// wavefronts owns one tile (up to 16*MAXRB rows of one expert); every wavefront streams one
+// weight matrix over one 16-column block: for the down projection 4 blocks per work-group,
+// for gate/up 2 column blocks with a gate wavefront and an up wavefront each, which swap
+// accumulators through LDS for the SwiGLU epilogue. The K loop runs in chunks of U k-steps:
+// the work-group stages the chunk's activation rows once in LDS (double-buffered, rows
+// padded by 16 bytes so the 16 row-lanes of a fragment read hit distinct banks), and each
+// wavefront loads only its weights from HBM, in plain load-then-use batches (the pattern
+// that measured closest to the HBM ceiling), reading activation fragments from LDS.
+template <int WF, int EPI, int U, int MAXRB>
+__device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int cgroup,
+                                            uint4 (&As)[2][16 * MAXRB * (U * 8 + 1)]) {
+    constexpr bool SWIGLU = EPI == EPI_SWIGLU;
+    constexpr bool GROUPED = (WF == YVMOE_W_INT4 || WF == YVMOE_W_FP8);
+    constexpr int ROWS = 16 * MAXRB;
+    constexpr int ROW_U4 = U * 8 + 1;            // uint4 per staged row (U*64 bf16 + pad)
+    constexpr int CHUNK_U4 = ROWS * U * 8;       // uint4 of one chunk
+    constexpr int PER_THREAD = CHUNK_U4 / 256;   // uint4 each thread stages per chunk
+    static_assert(CHUNK_U4 % 256 == 0, "chunk must split evenly over 256 threads");
+    static_assert(2 * ROWS * ROW_U4 * 16 >= 2 * 64 * MAXRB * 16, "LDS too small for the swap");
+    typedef BLoad<WF> BL;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int e = p.tile_seg[tile];
+    const int row0 = p.tile_row0[tile];
+    const int seg_end = p.seg_start[e + 1];
+    const int nvalid = min(ROWS, seg_end - row0);
+    const int nrb = (nvalid + 15) / 16;
+    const int mat = SWIGLU ? (wave & 1) : 0;  // 0: gate (or down), 1: up
+    const int col0 = SWIGLU ? (cgroup * 2 + (wave >> 1)) * 16 : (cgroup * 4 + wave) * 16;
+    const bool active = col0 < p.ncols;  // waves past the last column still stage and sync
+    const int n = min(col0, p.ncols - 16) + (lane & 15);
+    const int kl = (lane >> 4) * 16;
+    const int nks = p.K / 64;
+    const int nchunks = (nks + U - 1) / U;
+
+    // staging: thread t copies uint4 q = t + j*256 of each chunk: row q / (U*8), column q % (U*8)
+    const char* srow[PER_THREAD];
+    int sdst[PER_THREAD], scol[PER_THREAD];
+    bool sval[PER_THREAD];
+#pragma unroll
+    for (int j = 0; j < PER_THREAD; ++j) {
+        const int q = tid + j * 256;
+        const int r = q / (U * 8);
+        scol[j] = q % (U * 8);
+        sval[j] = r < nvalid;
+        srow[j] = (const char*)p.A + (long long)map_row(p, row0 + (sval[j] ? r : 0)) * p.lda * 2;
+        sdst[j] = r * ROW_U4 + scol[j];
+    }
+    auto stage_load = [&](int c, uint4 (&v)[PER_THREAD]) {
+#pragma unroll
+        for (int j = 0; j < PER_THREAD; ++j) {
+            const int kk = c * U * 64 + scol[j] * 8;  // element offset in the row
+            v[j] = (sval[j] && kk < p.K) ? *(const uint4*)(srow[j] + (size_t)kk * 2) : make_uint4(0, 0, 0, 0);
+        }
+    };
+    auto stage_store = [&](int buf, const uint4 (&v)[PER_THREAD]) {
+#pragma unroll
+        for (int j = 0; j < PER_THREAD; ++j) As[buf][sdst[j]] = v[j];
+    };
+
+    const long long e_off = (long long)e * p.b_stride;
+    const long long s_off = (long long)e * p.s_stride;
+    const void* S = mat ? p.S1 : p.S0;
+    const char* bptr = BL::ptr(mat ? p.B1 : p.B0, e_off, n, p.K, kl);
+    const float scl = b_scale<WF>(S, s_off, n, p.K, 0);
+
+    f32x4 acc[MAXRB];
+#pragma unroll
+    for (int rb = 0; rb < MAXRB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    {
+        uint4 v[PER_THREAD];
+        stage_load(0, v);
+        stage_store(0, v);
+    }
+    __syncthreads();
+    for (int c = 0; c < nchunks; ++c) {
+        const int ks0 = c * U;
+        typename BL::Raw bw[U];
+        float sg[U];
+        if (active) {
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int ks = min(ks0 + u, nks - 1);
+                BL::load(bw[u], bptr, ks * 64);
+                if constexpr (GROUPED) sg[u] = b_scale<WF>(S, s_off, n, p.K, ks * 64);
+                else sg[u] = scl;
+            }
+        }
+        uint4 nxt[PER_THREAD];
+        if (c + 1 < nchunks) stage_load(c + 1, nxt);
+        if (active) {
+            const uint4* arow = &As[c & 1][(lane & 15) * ROW_U4 + (lane >> 4) * 2];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (ks0 + u < nks) {
+                    Frag16 bf;
+                    BL::cvt(bw[u], sg[u], bf);
+#pragma unroll
+                    for (int rb = 0; rb < MAXRB; ++rb) {
+                        if (rb < nrb) {
+                            Frag16 af;
+                            af.u[0] = arow[rb * 16 * ROW_U4 + u * 8];
+                            af.u[1] = arow[rb * 16 * ROW_U4 + u * 8 + 1];
+                            acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af.v[0], bf.v[0], acc[rb], 0, 0, 0);
+                            acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af.v[1], bf.v[1], acc[rb], 0, 0, 0);
+                        }
+                    }
+                }
+            }
+        }
+        if (c + 1 < nchunks) stage_store((c + 1) & 1, nxt);
+        __syncthreads();
+    }
+
+    if constexpr (SWIGLU) {
+        // up wavefronts hand their accumulators to the gate wavefront of the same columns
+        float* xchg = (float*)&As[0][0];
+        if (mat == 1) {
+#pragma unroll
+            for (int rb = 0; rb < MAXRB; ++rb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xchg[(((wave >> 1) * MAXRB + rb) * 4 + i) * 64 + lane] = acc[rb][i];
+        }
+        __syncthreads();
+        if (mat == 0 && active) {
+#pragma unroll
+        for (int rb = 0; rb < MAXRB; ++rb) {
+            if (rb < nrb) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = row0 + rb * 16 + (lane >> 4) * 4 + i;
+                    if (r < seg_end) {
+                        const float g = round_bf16(acc[rb][i]);
+                        const float u = round_bf16(xchg[(((wave >> 1) * MAXRB + rb) * 4 + i) * 64 + lane]);
+                        const float sgl = round_bf16(silu(g));
+                        ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(sgl * u);
+                    }
+                }
+            }
+        }
+        }
+        __syncthreads();  // the exchange area is the next item's staging buffer
+    } else {
+        if (!active) return;
+#pragma unroll
+        for (int rb = 0; rb < MAXRB; ++rb) {
+            if (rb < nrb) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = row0 + rb * 16 + (lane >> 4) * 4 + i;
+                    if (r < seg_end)
+                        ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(acc[rb][i]);
+                }
+            }
+        }
+    }
+}
+
+// Persistent launch: work-group b processes items b, b + G, ... of the ntiles x ngroups
+// (tile fastest) item space, with G chosen by the host so each does the same count.
+template <int WF, int EPI, int U, int MAXRB>
+__global__ __launch_bounds__(256) void gemm_stream_kernel(GemmParams p, int ngroups) {
+    __shared__ uint4 As[2][16 * MAXRB * (U * 8 + 1)];
+    const int nt = *p.ntiles;
+    const int nitems = nt * ngroups;
+    for (int item = blockIdx.x; item < nitems; item += gridDim.x)
+        stream_item<WF, EPI, U, MAXRB>(p, item % nt, item / nt, As);
 }
 
 // ------------------------------------------------------------------ fp32 activations
@@ -457,7 +650,8 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
 // Segments: routed experts [0, E) from the routing offsets, then S shared experts of N
 // rows each after the N*k routed rows. Every segment is cut into 64-row tiles.
 __global__ __launch_bounds__(512) void build_tiles_kernel(const int* __restrict__ offsets, int E,
-                                                          int S, int N, int k, int* __restrict__ seg,
+                                                          int S, int N, int k, int tile_rows,
+                                                          int* __restrict__ seg,
                                                           int* __restrict__ tile_seg,
                                                           int* __restrict__ tile_row0,
                                                           int* __restrict__ ntiles) {
@@ -475,7 +669,7 @@ __global__ __launch_bounds__(512) void build_tiles_kernel(const int* __restrict_
         }
         seg[tid] = s0;
         if (tid == nseg - 1) seg[nseg] = s1;
-        nt = (s1 - s0 + kTileRows - 1) / kTileRows;
+        nt = (s1 - s0 + tile_rows - 1) / tile_rows;
     }
     sc[tid] = nt;
     __syncthreads();
@@ -489,7 +683,7 @@ __global__ __launch_bounds__(512) void build_tiles_kernel(const int* __restrict_
         const int start = sc[tid] - nt;
         for (int q = 0; q < nt; ++q) {
             tile_seg[start + q] = tid;
-            tile_row0[start + q] = s0 + q * kTileRows;
+            tile_row0[start + q] = s0 + q * tile_rows;
         }
     }
     if (tid == 511) *ntiles = sc[511];
@@ -606,10 +800,33 @@ __global__ __launch_bounds__(256) void reduce_splits_kernel(const float* __restr
     out[i] = s;
 }
 
+// Streaming (decode) form: one (tile, column group) item per work-group.
+template <int EPI, int U>
+int stream_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, const char* name) {
+    const int ngroups = (EPI == EPI_SWIGLU) ? ceil_div(p.ncols, 32) : ceil_div(p.ncols, 64);
+    const long long items = (long long)ntiles_max * ngroups;
+    if (items <= 0) return YVMOE_OK;
+#define YV_ST(WFV)                                                                           \
+    do {                                                                                     \
+        /* one item per work-group measured best; the kernel also runs persistent grids */ \
+        gemm_stream_kernel<WFV, EPI, U, 1><<<(unsigned)items, 256, 0, st>>>(p, ngroups);     \
+    } while (0)
+    switch (wf) {
+        case YVMOE_W_BF16: YV_ST(YVMOE_W_BF16); break;
+        case YVMOE_W_INT8: YV_ST(YVMOE_W_INT8); break;
+        case YVMOE_W_INT4: YV_ST(YVMOE_W_INT4); break;
+        case YVMOE_W_FP8: YV_ST(YVMOE_W_FP8); break;
+        default: set_error("unsupported weight format %d for bf16 activations", wf); return YVMOE_ERR_DTYPE;
+    }
+#undef YV_ST
+    YV_LAUNCH_CHECK(name);
+    return YVMOE_OK;
+}
+
 // Launches one GEMM: grid (tiles, column groups, K splits); NCB 16-column blocks per wave.
 template <int EPI>
 int gemm_dispatch(int act, int wf, GemmParams p, int ntiles_max, int ncb, int ksplit,
-                  hipStream_t st, const char* name) {
+                  hipStream_t st, const char* name, int maxrb = 4) {
     if (ntiles_max <= 0) return YVMOE_OK;
     if (p.ncols % (16 * ncb) != 0) {
         set_error("%s: %d columns are not a multiple of %d", name, p.ncols, 16 * ncb);
@@ -621,10 +838,15 @@ int gemm_dispatch(int act, int wf, GemmParams p, int ntiles_max, int ncb, int ks
         if (ncb == 2) gemm_f32_kernel<EPI, 2><<<grid, 256, 0, st>>>(p);
         else gemm_f32_kernel<EPI, 1><<<grid, 256, 0, st>>>(p);
     } else {
-#define YV_GB(WFV)                                                          \
-    do {                                                                    \
-        if (ncb == 2) gemm_bf16_kernel<WFV, EPI, 2><<<grid, 256, 0, st>>>(p); \
-        else gemm_bf16_kernel<WFV, EPI, 1><<<grid, 256, 0, st>>>(p);        \
+#define YV_GB(WFV)                                                                  \
+    do {                                                                            \
+        if (maxrb == 1) {                                                           \
+            if (ncb == 2) gemm_bf16_kernel<WFV, EPI, 2, 1><<<grid, 256, 0, st>>>(p); \
+            else gemm_bf16_kernel<WFV, EPI, 1, 1><<<grid, 256, 0, st>>>(p);         \
+        } else {                                                                    \
+            if (ncb == 2) gemm_bf16_kernel<WFV, EPI, 2, 4><<<grid, 256, 0, st>>>(p); \
+            else gemm_bf16_kernel<WFV, EPI, 1, 4><<<grid, 256, 0, st>>>(p);         \
+        }                                                                           \
     } while (0)
         switch (wf) {
             case YVMOE_W_BF16: YV_GB(YVMOE_W_BF16); break;
@@ -682,9 +904,13 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     int* tile_row0 = (int*)(fws + FL.tile_row0);
     int* ntiles = (int*)(fws + FL.ntiles);
     void* hbuf = fws + FL.h;
-    const int T = max_tiles(N, k, E, S);
-    build_tiles_kernel<<<1, 512, 0, st>>>(routing->offsets, E, S, N, k, seg, tile_seg, tile_row0,
-                                          ntiles);
+    // 16-row tiles (one MFMA row block per wave) when experts hold few rows (decode-like
+    // batches), 64-row tiles otherwise
+    const int maxrb = (act == YVMOE_ACT_BF16 && N * k <= 32 * E) ? 1 : 4;
+    const int tile_rows = 16 * maxrb;
+    const int T = max_tiles(N, k, E, S, tile_rows);
+    build_tiles_kernel<<<1, 512, 0, st>>>(routing->offsets, E, S, N, k, tile_rows, seg, tile_seg,
+                                          tile_row0, ntiles);
     YV_LAUNCH_CHECK("build_tiles");
     const int wf = w->format;
     GemmParams p{};
@@ -711,7 +937,10 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.out = hbuf;
     p.ldo = F;
     p.kchunk = H;
-    int rc = gemm_dispatch<EPI_SWIGLU>(act, wf, p, T, (F % 32 == 0) ? 2 : 1, 1, st, "expert_gemm1");
+    const bool streaming = (maxrb == 1);
+    int rc = streaming ? stream_dispatch<EPI_SWIGLU, 4>(wf, p, T, st, "expert_gemm1")
+                       : gemm_dispatch<EPI_SWIGLU>(act, wf, p, T, (F % 32 == 0) ? 2 : 1, 1, st,
+                                                   "expert_gemm1", maxrb);
     if (rc != YVMOE_OK) return rc;
     // GEMM2: y = h Wd^T (rows already in sorted order)
     p.A = hbuf;
@@ -730,7 +959,9 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.out = y;
     p.ldo = H;
     p.kchunk = F;
-    return gemm_dispatch<EPI_DOWN>(act, wf, p, T, (H % 32 == 0) ? 2 : 1, 1, st, "expert_gemm2");
+    return streaming ? stream_dispatch<EPI_DOWN, 4>(wf, p, T, st, "expert_gemm2")
+                     : gemm_dispatch<EPI_DOWN>(act, wf, p, T, (H % 32 == 0) ? 2 : 1, 1, st,
+                                               "expert_gemm2", maxrb);
 }
 
 int combine_launch(const void* y, int act, int N, int H, int k, int S, const yvmoe_routing* routing,

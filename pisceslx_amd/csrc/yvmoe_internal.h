@@ -59,9 +59,9 @@ inline size_t router_partials_bytes(int N, int E, int act, int H) {
     return ks > 1 ? align_up((size_t)ks * N * router_ld(E, act) * 4, 256) : 0;
 }
 
-// Upper bound on the number of 64-row GEMM tiles over all segments.
-inline int max_tiles(int N, int k, int E, int S) {
-    return ceil_div(N * k, kTileRows) + E + S * ceil_div(N, kTileRows);
+// Upper bound on the number of GEMM tiles of tile_rows rows over all segments.
+inline int max_tiles(int N, int k, int E, int S, int tile_rows) {
+    return ceil_div(N * k, tile_rows) + E + S * ceil_div(N, tile_rows);
 }
 
 // Workspace layout. The routing region depends on (N, E, k) only, so yvmoe_route and
@@ -92,7 +92,7 @@ inline RouteWs route_ws(int N, int E, int k) {
 inline FfnWs ffn_ws(int N, int k, int E, int S, int F, int act) {
     FfnWs w{};
     const size_t R = (size_t)N * k + (size_t)S * N;
-    const int T = max_tiles(N, k, E, S);
+    const int T = max_tiles(N, k, E, S, 16);  // 16-row tiles give the most tiles
     size_t o = 0;
     w.seg = o;       o = align_up(o + (size_t)(E + S + 1) * 4, 256);
     w.tile_seg = o;  o = align_up(o + (size_t)T * 4 + 4, 256);
