@@ -68,7 +68,20 @@ class YvStableMoEGate(nn.Module):
 
     # ------------------------------------------------------------ host-side state
     def _load_adjustment(self) -> Optional[torch.Tensor]:
-        """0.1 * (predicted - recent usage) of gate.py:1192-1209, or None when inactive."""
+        """0.1 * (predicted - recent usage) of gate.py:1192-1209, or None when inactive.
+
+        Computed on the host side from the routing-history buffers, which an inference forward
+        never changes, so the result is cached on the buffers' versions (no device sync per call).
+        """
+        key = tuple((b.data_ptr(), b._version) for b in (
+            self.history_ptr, self.load_buffer_ptr, self.routing_history, self.expert_load_buffer))
+        if getattr(self, "_adj_key", None) == key:
+            return self._adj
+        self._adj = self._compute_load_adjustment()
+        self._adj_key = key
+        return self._adj
+
+    def _compute_load_adjustment(self) -> Optional[torch.Tensor]:
         hp = int(self.history_ptr.item())
         if hp <= 0:
             return None

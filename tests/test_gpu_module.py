@@ -1,0 +1,130 @@
+"""The drop-in modules on the GPU: YvDeepSeekMoELayer loaded from a reference-style state
+dict, called the way YvHybridBlock calls it, against the CPU oracle; the stateful skip
+residual across calls (model/moe/layer.py:741-753, mirrored from
+tools/test/test_moe_routing_contract.py:187-201); the YvStableMoEGate contract
+(tools/test/test_moe_routing_contract.py:65-81)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle
+from pisceslx_amd import YvDeepSeekMoELayer, YvStableMoEGate
+from pisceslx_amd import functional as yvf
+
+from helpers import cosine
+
+pytestmark = pytest.mark.gpu
+
+
+class Cfg:
+    hidden_size = 256
+    intermediate_size = 384
+    moe_num_experts = 16
+    moe_top_k = 4
+    moe_shared_experts = 2
+    moe_min_capacity = 2
+    moe_fixed_shape_mode = False
+    diversity_weight = 0.0
+
+
+def reference_state_dict(cfg, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    H, F, E, S = cfg.hidden_size, cfg.intermediate_size, cfg.moe_num_experts, cfg.moe_shared_experts
+    r = lambda *s: torch.randn(*s, generator=g) * 0.02
+    sd = {}
+    for e in range(E):
+        for n, shp in (("gate", (F, H)), ("up", (F, H)), ("down", (H, F))):
+            sd[f"experts.{e}.{n}_proj.weight"] = r(*shp)
+    for s_ in range(S):
+        for n, shp in (("gate", (F, H)), ("up", (F, H)), ("down", (H, F))):
+            sd[f"shared_experts.{s_}.expert.{n}_proj.weight"] = r(*shp)
+    sd["shared_expert_weight"] = torch.ones(S) / S
+    sd["router.gate.weight"] = r(E, H)
+    sd["router.complexity_predictor.0.weight"] = r(64, H)
+    sd["router.complexity_predictor.0.bias"] = torch.zeros(64)
+    sd["router.complexity_predictor.2.weight"] = r(1, 64)
+    sd["router.complexity_predictor.2.bias"] = torch.zeros(1)
+    return sd
+
+
+def oracle_params_of(layer):
+    cpu = layer.experts_packed.to("cpu")
+    pred = layer.router.complexity_predictor
+    return moe_oracle.LayerParams(
+        hidden=layer.hidden_size, ffn=layer.intermediate_size, num_experts=layer.num_experts,
+        num_shared=layer.num_shared_experts, top_k=layer.top_k,
+        gate_weight=layer.router.gate.weight.detach().cpu(),
+        pred=(pred[0].weight.detach().cpu(), pred[0].bias.detach().cpu(),
+              pred[2].weight.detach().cpu(), pred[2].bias.detach().cpu()),
+        bias=None, fixed_shape_mode=False, dynamic_capacity=True,
+        capacity_factor=1.0, min_capacity=layer.router.min_capacity,
+        mix_param=layer.shared_expert_weight.detach().cpu(),
+        expert_fn=lambda i: cpu.dequantize(i, torch.float32))
+
+
+def _oracle_call(layer, x, skip):
+    x2d = x.reshape(-1, x.shape[-1])
+    st = layer.router.router_state(yvf._act(x2d.dtype))
+    lg = yvf.router_logits(x2d.contiguous(), st)[:, :layer.num_experts].cpu().numpy()
+    cap = int(layer.last_routing.capacity.item())
+    o = moe_oracle.layer_forward(x2d.cpu(), oracle_params_of(layer), logits=lg, cap=cap,
+                                 skip=None if skip is None else skip.reshape(x2d.shape).cpu())
+    assert cap == moe_oracle.layer_capacity(oracle_params_of(layer), x2d.cpu())
+    return o
+
+
+@pytest.mark.parametrize("fmt", ["int8", "bf16"])
+def test_deepseek_layer_drop_in(cuda, oracle, fmt):
+    cfg = Cfg()
+    layer = YvDeepSeekMoELayer(cfg, device=cuda, dtype=torch.bfloat16, weight_format=fmt).eval()
+    layer.load_reference_state_dict(reference_state_dict(cfg))
+    g = torch.Generator(device=cuda).manual_seed(1)
+    x1 = torch.randn(2, 17, cfg.hidden_size, device=cuda, generator=g).to(torch.bfloat16)
+    x2 = torch.randn(2, 17, cfg.hidden_size, device=cuda, generator=g).to(torch.bfloat16)
+    x3 = torch.randn(1, 9, cfg.hidden_size, device=cuda, generator=g).to(torch.bfloat16)
+
+    print(f"module drop-in fmt={fmt}", flush=True)
+    out1, loss = layer(x1, modal_id=torch.zeros(2, dtype=torch.long, device=cuda))
+    torch.cuda.synchronize()
+    assert out1.shape == x1.shape and float(loss) == 0.0
+    out1 = out1.reshape(-1, cfg.hidden_size)
+    o1 = _oracle_call(layer, x1, None)
+    assert cosine(out1.cpu(), o1["out"]) >= 0.9999
+    assert float((out1.cpu().double() - o1["out"].double()).abs().max()) <= 2e-2
+    skip1 = layer._skip_buffer.clone()
+
+    out2, _ = layer(x2)                     # same shape: adds 0.1 * previous shared output
+    torch.cuda.synchronize()
+    out2 = out2.reshape(-1, cfg.hidden_size)
+    o2 = _oracle_call(layer, x2, skip1)
+    assert cosine(out2.cpu(), o2["out"]) >= 0.9999
+    assert float((out2.cpu().double() - o2["out"].double()).abs().max()) <= 2e-2
+    no_skip = _oracle_call(layer, x2, None)["out"]
+    assert float((out2.cpu().float() - no_skip.float()).abs().max()) > 1e-3  # the residual is there
+
+    out3, _ = layer(x3)                     # shape change: no residual from the 2x17 batch
+    torch.cuda.synchronize()
+    assert out3.shape == x3.shape
+    out3 = out3.reshape(-1, cfg.hidden_size)
+    o3 = _oracle_call(layer, x3, None)
+    assert cosine(out3.cpu(), o3["out"]) >= 0.9999
+
+
+def test_stable_gate_contract(cuda, oracle):
+    gate = YvStableMoEGate(hidden_size=64, num_experts=4, top_k=2, capacity_factor=1.0,
+                           min_capacity=1, device=cuda).eval()
+    x = torch.randn(1, 24, 64, device=cuda)
+    weights, indices, loss = gate(x)
+    torch.cuda.synchronize()
+    assert weights.shape == (24, 2) and indices.shape == (24, 2)
+    assert indices.dtype == torch.int64 and float(loss) == 0.0
+    tot = weights.sum(-1)
+    assert bool(torch.all((tot <= 1.0 + 1e-5) | (tot == 0))) and bool(torch.all(weights >= 0))
+    with pytest.raises(NotImplementedError):
+        gate.train()(x)
+
+
+def test_layer_rejects_training_mode(cuda):
+    layer = YvDeepSeekMoELayer(Cfg(), device=cuda, dtype=torch.bfloat16, weight_format="bf16")
+    with pytest.raises(NotImplementedError):
+        layer.train()(torch.randn(1, 4, Cfg.hidden_size, device=cuda).to(torch.bfloat16))
