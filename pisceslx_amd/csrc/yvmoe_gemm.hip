@@ -35,6 +35,7 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));  // staging registers (plain vector)
 
 enum Epi { EPI_F32 = 0, EPI_SWIGLU = 1, EPI_DOWN = 2 };
 
@@ -553,6 +554,224 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(GemmParams p, int ngro
         stream_item<WF, EPI, U, MAXRB>(p, item % nt, item / nt, As);
 }
 
+// ------------------------------------------------------------------ bf16, LDS-tiled form
+// Tiled form for batches whose experts hold many rows (prefill). A work-group of 8
+// wavefronts computes a 256-row x 256-column output tile over K in 64-wide chunks,
+// double-buffered in LDS (2 x 64 KB): the activation rows are gathered through the
+// permutation, the weight tile is dequantized once to bf16(q * s) on its way into LDS, and
+// each wavefront (2 x 4 layout) computes 128 rows x 64 columns from LDS fragments. For
+// gate/up the weight tile is 128 gate rows then the 128 up rows of the same 128 columns; each
+// wavefront holds gate and up of its 32 columns and finishes SwiGLU in registers.
+//
+// Per 64-wide K chunk a wavefront issues 24 fragment reads and 64 MFMAs; the work-group
+// writes 64 KB of LDS and dequantizes 16 K weights, half the per-flop LDS and VALU work of a
+// 128 x 128 tile.
+constexpr int TBM = 256, TBN = 256, TBK = 64;
+constexpr int TROW = TBK;  // bf16 per LDS row (128 bytes)
+constexpr int TTHREADS = 512;
+// LDS swizzle: the 16-byte chunk c of row r is stored at chunk c ^ (r & 7). A fragment read
+// (16 rows, one chunk each) then touches 16 distinct chunk positions and runs without bank
+// conflicts; the plain and the 16-byte-padded layouts measured 4x and 2x slower reads.
+__device__ __forceinline__ int swz(int row, int chunk) { return row * TROW + ((chunk ^ (row & 7)) << 3); }
+
+// Activation tile loader: 256 rows x 64 k of one chunk (rows gathered through the
+// permutation; rows past the segment end read the tile's first row), 8 threads per row,
+// thread t covers row t / 8 + 64 j, chunk t % 8.
+struct TileA {
+    u32x4 raw[4];
+    const char* base[4];
+    __device__ void init(const GemmParams& p, int row0, int seg_end) {
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = row0 + t / 8 + 64 * j;
+            base[j] = (const char*)p.A + ((long long)map_row(p, r < seg_end ? r : row0) * p.lda + (t % 8) * 8) * 2;
+        }
+    }
+    __device__ void load(int k0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) raw[j] = *(const u32x4*)(base[j] + (size_t)k0 * 2);
+    }
+    __device__ void store(unsigned short* lds) const {
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) *(u32x4*)(lds + swz(t / 8 + 64 * j, t % 8)) = raw[j];
+    }
+};
+
+// Weight tile loader: 256 rows x 64 k of one chunk, global -> registers (16-byte loads, TPR
+// threads per row) -> bf16(q * s) into LDS. Thread t covers row t / TPR + (512 / TPR) j.
+template <int WF>
+struct TileB {
+    static constexpr int EB = (WF == YVMOE_W_BF16) ? 2 : 1;  // bytes per weight
+    static constexpr int TPR = TBK * EB / 16;                 // threads per row
+    static constexpr int PT = TBN * TPR / TTHREADS;           // rows per thread
+    u32x4 raw[PT];
+    const char* base;
+    long long rstride[PT];
+    int row[PT];
+    __device__ void init(const GemmParams& p, long long e_off, int n0, bool swiglu) {
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int j = 0; j < PT; ++j) row[j] = t / TPR + (TTHREADS / TPR) * j;
+        // rows of one matrix are contiguous: one base pointer plus per-row offsets
+        base = (const char*)p.B0 + (e_off + (long long)n0 * p.K) * EB + (t % TPR) * 16;
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+            if (swiglu && row[j] >= TBN / 2)
+                rstride[j] = ((const char*)p.B1 - (const char*)p.B0) + (long long)(row[j] - TBN / 2) * p.K * EB;
+            else
+                rstride[j] = (long long)row[j] * p.K * EB;
+        }
+    }
+    __device__ void load(int k0) {
+#pragma unroll
+        for (int j = 0; j < PT; ++j) raw[j] = *(const u32x4*)(base + rstride[j] + (size_t)k0 * EB);
+    }
+    __device__ void store(unsigned short* lds, const float (&scale)[PT]) const {
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int j = 0; j < PT; ++j) {
+            if constexpr (EB == 2) {
+                *(u32x4*)(lds + swz(row[j], t % TPR)) = raw[j];
+            } else {
+                Frag16 f;
+                BLoad<WF>::cvt(make_uint4(raw[j].x, raw[j].y, raw[j].z, raw[j].w), scale[j], f);
+                *(u32x4*)(lds + swz(row[j], 2 * (t % TPR))) = u32x4{f.u[0].x, f.u[0].y, f.u[0].z, f.u[0].w};
+                *(u32x4*)(lds + swz(row[j], 2 * (t % TPR) + 1)) = u32x4{f.u[1].x, f.u[1].y, f.u[1].z, f.u[1].w};
+            }
+        }
+    }
+};
+
+// Work items are (tile, column block) pairs, column block fastest, so the work-groups that
+// run together share activation tiles and (mostly) one expert's weights. Consecutive
+// work-group ids go to different XCDs (round-robin dispatch), so the item space is cut into 8
+// contiguous ranges, one per XCD, to keep each XCD's L2 traffic on its own range.
+template <int WF, int EPI>
+__global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int ncb) {
+    constexpr bool SWIGLU = EPI == EPI_SWIGLU;
+    constexpr bool GROUPED = (WF == YVMOE_W_INT4 || WF == YVMOE_W_FP8);
+    static_assert(WF == YVMOE_W_INT8 || WF == YVMOE_W_FP8 || WF == YVMOE_W_BF16,
+                  "tiled form covers 1- and 2-byte weight formats");
+    __shared__ unsigned short As[2][TBM * TROW];
+    __shared__ unsigned short Bs[2][TBN * TROW];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int wr = wave >> 2, wc = wave & 3;
+    const int total = *p.ntiles * ncb;
+    const int per_xcd = (total + 7) / 8;
+    const int local = blockIdx.x / 8;
+    if (local >= per_xcd) return;
+    const int item = (blockIdx.x % 8) * per_xcd + local;
+    if (item >= total) return;
+    const int tile = item / ncb;
+    const int cb = item % ncb;
+    const int e = p.tile_seg[tile];
+    const int row0 = p.tile_row0[tile];
+    const int seg_end = p.seg_start[e + 1];
+    // output columns: gate/up -> 128 columns (x2 matrices); down -> 256 columns
+    const int n0 = SWIGLU ? cb * (TBN / 2) : cb * TBN;
+    const int nks = p.K / TBK;
+    const long long e_off = (long long)e * p.b_stride;
+    const long long s_off = (long long)e * p.s_stride;
+
+    TileA ta;
+    ta.init(p, row0, seg_end);
+    typedef TileB<WF> TB;
+    TB tb;
+    float bscale[TB::PT];
+    tb.init(p, e_off, n0, SWIGLU);
+    auto b_scales = [&](int c) {
+#pragma unroll
+        for (int j = 0; j < TB::PT; ++j) {
+            const int r = tb.row[j];
+            const void* S = (SWIGLU && r >= TBN / 2) ? p.S1 : p.S0;
+            const int n = SWIGLU ? n0 + (r & (TBN / 2 - 1)) : n0 + r;
+            bscale[j] = b_scale<WF>(S, s_off, n, p.K, c * TBK);
+        }
+    };
+
+    f32x4 acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // fragment offsets (elements) of k-half 0; k-half 1 is chunk + 4, i.e. offset ^ 32
+    const int a_off = swz(wr * 128 + (lane & 15), lane >> 4);
+    int b_off[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+        const int brow = SWIGLU ? ((nb < 2) ? wc * 32 + nb * 16 : TBN / 2 + wc * 32 + (nb - 2) * 16)
+                                : wc * 64 + nb * 16;
+        b_off[nb] = swz(brow + (lane & 15), lane >> 4);
+    }
+
+    ta.load(0);
+    tb.load(0);
+    b_scales(0);
+    ta.store(As[0]);
+    tb.store(Bs[0], bscale);
+    __syncthreads();
+    for (int c = 0; c < nks; ++c) {
+        const int cur = c & 1;
+        // the next chunk's loads are unconditional (the last iteration reloads its own chunk
+        // into the idle buffer): no branch around them, so they stay in flight over the MFMAs
+        const int cn = min(c + 1, nks - 1);
+        ta.load(cn * TBK);
+        tb.load(cn * TBK);
+        if constexpr (GROUPED) b_scales(cn);
+        // keep the scheduler from sinking the loads below the MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            bf16x8 bfv[4];
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb)
+                bfv[nb] = *(const bf16x8*)(&Bs[cur][b_off[nb] ^ (ks * 32)]);
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb) {
+                const bf16x8 af = *(const bf16x8*)(&As[cur][(a_off + mb * 16 * TROW) ^ (ks * 32)]);
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb)
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfv[nb], acc[mb][nb], 0, 0, 0);
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        ta.store(As[cur ^ 1]);
+        tb.store(Bs[cur ^ 1], bscale);
+        __syncthreads();
+    }
+
+    // epilogue: lane holds rows 4*(l/16)+i of each 16-row block, column l%16 of each block
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = row0 + wr * 128 + mb * 16 + (lane >> 4) * 4 + i;
+            if (r >= seg_end) continue;
+            if constexpr (SWIGLU) {
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+                    const int n = n0 + wc * 32 + nb * 16 + (lane & 15);
+                    const float g = round_bf16(acc[mb][nb][i]);
+                    const float u = round_bf16(acc[mb][nb + 2][i]);
+                    const float sgl = round_bf16(silu(g));
+                    ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(sgl * u);
+                }
+            } else {
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb) {
+                    const int n = n0 + wc * 64 + nb * 16 + (lane & 15);
+                    ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(acc[mb][nb][i]);
+                }
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ fp32 activations
 // fp32 activations and fp32 weights (the reference's fp32 configuration).
 template <int EPI, int NCB>
@@ -823,6 +1042,28 @@ int stream_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st,
     return YVMOE_OK;
 }
 
+// LDS-tiled (prefill) form: one work-group per (256-row tile, column block of 128 (gate/up)
+// or 256 (down)); grid = 8 x per-XCD range, sized for the most tiles the batch can have.
+template <int EPI>
+int tile_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, const char* name) {
+    const int cols = (EPI == EPI_SWIGLU) ? TBN / 2 : TBN;
+    if (p.ncols % cols != 0 || p.K % TBK != 0) {
+        set_error("%s: tiled form needs columns %% %d == 0 and K %% %d == 0", name, cols, TBK);
+        return YVMOE_ERR_SHAPE;
+    }
+    if (ntiles_max <= 0) return YVMOE_OK;
+    const int ncb = p.ncols / cols;
+    const long long blocks = 8LL * ceil_div(ntiles_max * ncb, 8);
+    switch (wf) {
+        case YVMOE_W_BF16: gemm_tile_kernel<YVMOE_W_BF16, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
+        case YVMOE_W_INT8: gemm_tile_kernel<YVMOE_W_INT8, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
+        case YVMOE_W_FP8: gemm_tile_kernel<YVMOE_W_FP8, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
+        default: set_error("%s: no tiled form for weight format %d", name, wf); return YVMOE_ERR_DTYPE;
+    }
+    YV_LAUNCH_CHECK(name);
+    return YVMOE_OK;
+}
+
 // Launches one GEMM: grid (tiles, column groups, K splits); NCB 16-column blocks per wave.
 template <int EPI>
 int gemm_dispatch(int act, int wf, GemmParams p, int ntiles_max, int ncb, int ksplit,
@@ -907,7 +1148,10 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     // 16-row tiles (one MFMA row block per wave) when experts hold few rows (decode-like
     // batches), 64-row tiles otherwise
     const int maxrb = (act == YVMOE_ACT_BF16 && N * k <= 32 * E) ? 1 : 4;
-    const int tile_rows = 16 * maxrb;
+    // 256-row LDS-tiled form when experts hold many rows (prefill-like batches)
+    const bool tiled = act == YVMOE_ACT_BF16 && N * k >= 64 * E && F % (TBN / 2) == 0 && H % TBN == 0 &&
+                       (w->format == YVMOE_W_INT8 || w->format == YVMOE_W_FP8 || w->format == YVMOE_W_BF16);
+    const int tile_rows = tiled ? TBM : 16 * maxrb;
     const int T = max_tiles(N, k, E, S, tile_rows);
     build_tiles_kernel<<<1, 512, 0, st>>>(routing->offsets, E, S, N, k, tile_rows, seg, tile_seg,
                                           tile_row0, ntiles);
@@ -938,7 +1182,8 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.ldo = F;
     p.kchunk = H;
     const bool streaming = (maxrb == 1);
-    int rc = streaming ? stream_dispatch<EPI_SWIGLU, 4>(wf, p, T, st, "expert_gemm1")
+    int rc = tiled ? tile_dispatch<EPI_SWIGLU>(wf, p, T, st, "expert_gemm1")
+           : streaming ? stream_dispatch<EPI_SWIGLU, 4>(wf, p, T, st, "expert_gemm1")
                        : gemm_dispatch<EPI_SWIGLU>(act, wf, p, T, (F % 32 == 0) ? 2 : 1, 1, st,
                                                    "expert_gemm1", maxrb);
     if (rc != YVMOE_OK) return rc;
@@ -959,6 +1204,7 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.out = y;
     p.ldo = H;
     p.kchunk = F;
+    if (tiled) return tile_dispatch<EPI_DOWN>(wf, p, T, st, "expert_gemm2");
     return streaming ? stream_dispatch<EPI_DOWN, 4>(wf, p, T, st, "expert_gemm2")
                      : gemm_dispatch<EPI_DOWN>(act, wf, p, T, (H % 32 == 0) ? 2 : 1, 1, st,
                                                "expert_gemm2", maxrb);

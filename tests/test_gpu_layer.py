@@ -130,6 +130,16 @@ def test_bf16_and_small_shapes(cuda, oracle):
     _run_and_check(oracle, w)
 
 
+def test_bf16_tiled_prefill_shapes(cuda, oracle):
+    # unquantized bf16 experts with many rows per expert (the 128-row LDS-tiled GEMMs), segment
+    # ends inside tiles
+    from pisceslx_amd import _lib
+    from pisceslx_amd.workloads import LayerSpec
+    spec = LayerSpec("tiled_bf16", 256, 384, 4, 2, 1, _lib.W_BF16, torch.bfloat16)
+    w = make_workload(spec, device="cuda", lengths=[200, 77, 3])
+    _run_and_check(oracle, w)
+
+
 def test_forward_is_deterministic(cuda, oracle):
     w = make_workload("cfg3", device="cuda", n_tokens=700)
     st = router_state(w)
