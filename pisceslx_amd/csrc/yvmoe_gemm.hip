@@ -556,92 +556,58 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(GemmParams p, int ngro
 
 // ------------------------------------------------------------------ bf16, LDS-tiled form
 // Tiled form for batches whose experts hold many rows (prefill). A work-group of 8
-// wavefronts computes a 256-row x 256-column output tile over K in 64-wide chunks,
-// double-buffered in LDS (2 x 64 KB): the activation rows are gathered through the
-// permutation, the weight tile is dequantized once to bf16(q * s) on its way into LDS, and
-// each wavefront (2 x 4 layout) computes 128 rows x 64 columns from LDS fragments. For
-// gate/up the weight tile is 128 gate rows then the 128 up rows of the same 128 columns; each
-// wavefront holds gate and up of its 32 columns and finishes SwiGLU in registers.
+// wavefronts computes a 256-row x 256-column output tile over K in 64-wide chunks.
 //
-// Per 64-wide K chunk a wavefront issues 24 fragment reads and 64 MFMAs; the work-group
-// writes 64 KB of LDS and dequantizes 16 K weights, half the per-flop LDS and VALU work of a
-// 128 x 128 tile.
+// Chunks travel HBM -> LDS by direct-to-LDS loads (global_load_lds_dwordx4: each lane names
+// its own 16-byte source, the wavefront's 64 lanes fill 1 KB of LDS in lane order), two
+// chunks ahead of the MFMAs through a 3-stage LDS ring, with no register staging: the
+// activation rows are gathered through the permutation, the weights land as stored (1-byte
+// codes or bf16). Each wavefront owns 32 weight rows (1 x 8 layout: all 256 rows x 32
+// columns), reads its weight fragment once per chunk, dequantizes it to bf16(q * s) in
+// registers and multiplies it against the 16 activation row blocks. For gate/up the weight
+// tile is 128 gate rows then the 128 up rows of the same columns; wavefront w holds gate and
+// up of columns 16 w .. 16 w + 15 and finishes SwiGLU in registers.
+//
+// Each lane's MFMA operands cover 16 consecutive k of the chunk (k group l / 16), split over
+// the two MFMAs of a chunk in the same order for both operands. LDS layouts are swizzled in
+// 16-byte chunks so the fragment reads run without bank conflicts (measured): activation
+// rows (128 B) put chunk c of row r at c ^ (r & 7) ^ ((r >> 3) & 1), 1-byte weight rows
+// (64 B) put chunk c at c ^ ((r >> 1) & 3). The writes follow from the lane order of the
+// direct loads: lane L of a 1 KB block fetches the logical chunk that the swizzle places at
+// position L.
 constexpr int TBM = 256, TBN = 256, TBK = 64;
-constexpr int TROW = TBK;  // bf16 per LDS row (128 bytes)
 constexpr int TTHREADS = 512;
-// LDS swizzle: the 16-byte chunk c of row r is stored at chunk c ^ (r & 7). A fragment read
-// (16 rows, one chunk each) then touches 16 distinct chunk positions and runs without bank
-// conflicts; the plain and the 16-byte-padded layouts measured 4x and 2x slower reads.
-__device__ __forceinline__ int swz(int row, int chunk) { return row * TROW + ((chunk ^ (row & 7)) << 3); }
 
-// Activation tile loader: 256 rows x 64 k of one chunk (rows gathered through the
-// permutation; rows past the segment end read the tile's first row), 8 threads per row,
-// thread t covers row t / 8 + 64 j, chunk t % 8.
-struct TileA {
-    u32x4 raw[4];
-    const char* base[4];
-    __device__ void init(const GemmParams& p, int row0, int seg_end) {
-        const int t = threadIdx.x;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int r = row0 + t / 8 + 64 * j;
-            base[j] = (const char*)p.A + ((long long)map_row(p, r < seg_end ? r : row0) * p.lda + (t % 8) * 8) * 2;
-        }
-    }
-    __device__ void load(int k0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) raw[j] = *(const u32x4*)(base[j] + (size_t)k0 * 2);
-    }
-    __device__ void store(unsigned short* lds) const {
-        const int t = threadIdx.x;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) *(u32x4*)(lds + swz(t / 8 + 64 * j, t % 8)) = raw[j];
-    }
-};
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(1))) void* gbl_ptr_t;
 
-// Weight tile loader: 256 rows x 64 k of one chunk, global -> registers (16-byte loads, TPR
-// threads per row) -> bf16(q * s) into LDS. Thread t covers row t / TPR + (512 / TPR) j.
+// Direct-to-LDS load of 16 bytes per lane: lane L's bytes land at dst + 16 L (dst is the
+// same for the whole wavefront and goes to M0).
+__device__ __forceinline__ void dma16(const void* src, void* dst) {
+    const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_ptr_t)dst);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(src) : "memory", "m0");
+}
+
+__device__ __forceinline__ int swz_a(int r, int c) {  // bytes, 128-byte rows
+    return r * 128 + ((c ^ (r & 7) ^ ((r >> 3) & 1)) << 4);
+}
+__device__ __forceinline__ int swz_b(int r, int c) {  // bytes, 64-byte rows
+    return r * 64 + ((c ^ ((r >> 1) & 3)) << 4);
+}
+
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in bits 3:0 and
+// 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima)
+constexpr int vmcnt_only(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
+
 template <int WF>
-struct TileB {
+struct TileCfg {
     static constexpr int EB = (WF == YVMOE_W_BF16) ? 2 : 1;  // bytes per weight
-    static constexpr int TPR = TBK * EB / 16;                 // threads per row
-    static constexpr int PT = TBN * TPR / TTHREADS;           // rows per thread
-    u32x4 raw[PT];
-    const char* base;
-    long long rstride[PT];
-    int row[PT];
-    __device__ void init(const GemmParams& p, long long e_off, int n0, bool swiglu) {
-        const int t = threadIdx.x;
-#pragma unroll
-        for (int j = 0; j < PT; ++j) row[j] = t / TPR + (TTHREADS / TPR) * j;
-        // rows of one matrix are contiguous: one base pointer plus per-row offsets
-        base = (const char*)p.B0 + (e_off + (long long)n0 * p.K) * EB + (t % TPR) * 16;
-#pragma unroll
-        for (int j = 0; j < PT; ++j) {
-            if (swiglu && row[j] >= TBN / 2)
-                rstride[j] = ((const char*)p.B1 - (const char*)p.B0) + (long long)(row[j] - TBN / 2) * p.K * EB;
-            else
-                rstride[j] = (long long)row[j] * p.K * EB;
-        }
-    }
-    __device__ void load(int k0) {
-#pragma unroll
-        for (int j = 0; j < PT; ++j) raw[j] = *(const u32x4*)(base + rstride[j] + (size_t)k0 * EB);
-    }
-    __device__ void store(unsigned short* lds, const float (&scale)[PT]) const {
-        const int t = threadIdx.x;
-#pragma unroll
-        for (int j = 0; j < PT; ++j) {
-            if constexpr (EB == 2) {
-                *(u32x4*)(lds + swz(row[j], t % TPR)) = raw[j];
-            } else {
-                Frag16 f;
-                BLoad<WF>::cvt(make_uint4(raw[j].x, raw[j].y, raw[j].z, raw[j].w), scale[j], f);
-                *(u32x4*)(lds + swz(row[j], 2 * (t % TPR))) = u32x4{f.u[0].x, f.u[0].y, f.u[0].z, f.u[0].w};
-                *(u32x4*)(lds + swz(row[j], 2 * (t % TPR) + 1)) = u32x4{f.u[1].x, f.u[1].y, f.u[1].z, f.u[1].w};
-            }
-        }
-    }
+    static constexpr int NST = (EB == 2) ? 2 : 3;             // LDS stages (160 KB of LDS)
+    static constexpr int A_BYTES = TBM * TBK * 2;
+    static constexpr int B_BYTES = TBN * TBK * EB;
+    static constexpr int A_DMA = A_BYTES / 1024 / 8;  // 1 KB direct loads per wavefront
+    static constexpr int B_DMA = B_BYTES / 1024 / 8;
+    static constexpr int NPW = A_DMA + B_DMA;
 };
 
 // Work items are (tile, column block) pairs, column block fastest, so the work-groups that
@@ -650,16 +616,17 @@ struct TileB {
 // contiguous ranges, one per XCD, to keep each XCD's L2 traffic on its own range.
 template <int WF, int EPI>
 __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int ncb) {
+    typedef TileCfg<WF> C;
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
-    constexpr bool GROUPED = (WF == YVMOE_W_INT4 || WF == YVMOE_W_FP8);
+    constexpr bool GROUPED = WF == YVMOE_W_FP8;
     static_assert(WF == YVMOE_W_INT8 || WF == YVMOE_W_FP8 || WF == YVMOE_W_BF16,
                   "tiled form covers 1- and 2-byte weight formats");
-    __shared__ unsigned short As[2][TBM * TROW];
-    __shared__ unsigned short Bs[2][TBN * TROW];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds_a[C::NST][C::A_BYTES];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds_b[C::NST][C::B_BYTES];
+    __shared__ float lds_s[2][64];  // fp8: block scales of the tile's two 128-row weight blocks
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
-    const int wr = wave >> 2, wc = wave & 3;
     const int total = *p.ntiles * ncb;
     const int per_xcd = (total + 7) / 8;
     const int local = blockIdx.x / 8;
@@ -677,94 +644,157 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     const long long e_off = (long long)e * p.b_stride;
     const long long s_off = (long long)e * p.s_stride;
 
-    TileA ta;
-    ta.init(p, row0, seg_end);
-    typedef TileB<WF> TB;
-    TB tb;
-    float bscale[TB::PT];
-    tb.init(p, e_off, n0, SWIGLU);
-    auto b_scales = [&](int c) {
+    // direct-load sources: activation block j of this wavefront holds tile rows 8 (A_DMA w + j)
+    // .. + 7, lane L row + L / 8, logical chunk (L % 8) ^ (L / 8) ^ (block & 1)
+    const char* a_src[C::A_DMA];
 #pragma unroll
-        for (int j = 0; j < TB::PT; ++j) {
-            const int r = tb.row[j];
-            const void* S = (SWIGLU && r >= TBN / 2) ? p.S1 : p.S0;
-            const int n = SWIGLU ? n0 + (r & (TBN / 2 - 1)) : n0 + r;
-            bscale[j] = b_scale<WF>(S, s_off, n, p.K, c * TBK);
+    for (int j = 0; j < C::A_DMA; ++j) {
+        const int blk = wave * C::A_DMA + j;
+        const int r = blk * 8 + lane / 8;
+        const int lc = (lane % 8) ^ (lane / 8) ^ (blk & 1);
+        const int gr = (row0 + r < seg_end) ? row0 + r : row0;
+        a_src[j] = (const char*)p.A + ((long long)map_row(p, gr) * p.lda + lc * 8) * 2;
+    }
+    const char* b_src[C::B_DMA];
+#pragma unroll
+    for (int j = 0; j < C::B_DMA; ++j) {
+        const int blk = wave * C::B_DMA + j;
+        int r, lc;
+        if constexpr (C::EB == 1) {
+            r = blk * 16 + lane / 4;
+            lc = (lane % 4) ^ ((r >> 1) & 3);
+        } else {
+            r = blk * 8 + lane / 8;
+            lc = (lane % 8) ^ (r & 7) ^ ((r >> 3) & 1);
         }
-    };
-
-    f32x4 acc[8][4];
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // fragment offsets (elements) of k-half 0; k-half 1 is chunk + 4, i.e. offset ^ 32
-    const int a_off = swz(wr * 128 + (lane & 15), lane >> 4);
-    int b_off[4];
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-        const int brow = SWIGLU ? ((nb < 2) ? wc * 32 + nb * 16 : TBN / 2 + wc * 32 + (nb - 2) * 16)
-                                : wc * 64 + nb * 16;
-        b_off[nb] = swz(brow + (lane & 15), lane >> 4);
+        const void* B = (SWIGLU && r >= TBN / 2) ? p.B1 : p.B0;
+        const int n = SWIGLU ? n0 + (r & (TBN / 2 - 1)) : n0 + r;
+        b_src[j] = (const char*)B + (e_off + (long long)n * p.K) * C::EB + lc * 16;
     }
 
-    ta.load(0);
-    tb.load(0);
-    b_scales(0);
-    ta.store(As[0]);
-    tb.store(Bs[0], bscale);
-    __syncthreads();
-    for (int c = 0; c < nks; ++c) {
-        const int cur = c & 1;
-        // the next chunk's loads are unconditional (the last iteration reloads its own chunk
-        // into the idle buffer): no branch around them, so they stay in flight over the MFMAs
-        const int cn = min(c + 1, nks - 1);
-        ta.load(cn * TBK);
-        tb.load(cn * TBK);
-        if constexpr (GROUPED) b_scales(cn);
-        // keep the scheduler from sinking the loads below the MFMAs
-        __builtin_amdgcn_sched_barrier(0);
+    // this lane's weight rows in the tile (fragment column l % 16 of each 16-row block)
+    int brow[2];
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            bf16x8 bfv[4];
+    for (int nb = 0; nb < 2; ++nb)
+        brow[nb] = SWIGLU ? nb * (TBN / 2) + wave * 16 + (lane & 15) : wave * 32 + nb * 16 + (lane & 15);
+    float cs[2] = {1.0f, 1.0f};  // int8: per-column scales
+    int sblk[2] = {0, 0};        // fp8: which of the tile's two scale blocks
+    if constexpr (WF == YVMOE_W_INT8) {
 #pragma unroll
-            for (int nb = 0; nb < 4; ++nb)
-                bfv[nb] = *(const bf16x8*)(&Bs[cur][b_off[nb] ^ (ks * 32)]);
-#pragma unroll
-            for (int mb = 0; mb < 8; ++mb) {
-                const bf16x8 af = *(const bf16x8*)(&As[cur][(a_off + mb * 16 * TROW) ^ (ks * 32)]);
-#pragma unroll
-                for (int nb = 0; nb < 4; ++nb)
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfv[nb], acc[mb][nb], 0, 0, 0);
-            }
+        for (int nb = 0; nb < 2; ++nb) {
+            const int r = brow[nb];
+            const void* S = (SWIGLU && r >= TBN / 2) ? p.S1 : p.S0;
+            cs[nb] = b_scale<WF>(S, s_off, SWIGLU ? n0 + (r & (TBN / 2 - 1)) : n0 + r, p.K, 0);
         }
-        __builtin_amdgcn_sched_barrier(0);
-        ta.store(As[cur ^ 1]);
-        tb.store(Bs[cur ^ 1], bscale);
+    }
+    if constexpr (GROUPED) {
+        const int kb = p.K / 128;
+        if (t < 2 * kb) {
+            const int b = t / kb, q = t % kb;
+            const void* S = (SWIGLU && b == 1) ? p.S1 : p.S0;
+            const int n = SWIGLU ? n0 : n0 + b * 128;
+            lds_s[b][q] = b_scale<WF>(S, s_off, n, p.K, q * 128);
+        }
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) sblk[nb] = brow[nb] / 128;
         __syncthreads();
     }
 
+    f32x4 acc[16][2];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // LDS byte offsets of this lane's fragment reads (k group g = lane / 16)
+    const int g = lane >> 4;
+    const int a_rd0 = swz_a(lane & 15, 2 * g), a_rd1 = swz_a(lane & 15, 2 * g + 1);
+    int b_rd0[2], b_rd1[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        if constexpr (C::EB == 1) {
+            b_rd0[nb] = swz_b(brow[nb], g);
+            b_rd1[nb] = 0;
+        } else {
+            b_rd0[nb] = swz_a(brow[nb], 2 * g);
+            b_rd1[nb] = swz_a(brow[nb], 2 * g + 1);
+        }
+    }
+
+    // The direct loads are issued from inline assembly: the compiler's own form of them makes
+    // it wait for every outstanding direct load before each LDS read, which would serialize
+    // the prefetch. Completion is tracked here instead, with explicit vmcnt waits.
+#define YV_TILE_ISSUE(CHUNK, ST)                                                                       \
+    do {                                                                                               \
+        _Pragma("unroll") for (int j = 0; j < C::A_DMA; ++j)                                           \
+            dma16(a_src[j] + (size_t)(CHUNK) * TBK * 2, &lds_a[ST][(wave * C::A_DMA + j) * 1024]);     \
+        _Pragma("unroll") for (int j = 0; j < C::B_DMA; ++j)                                           \
+            dma16(b_src[j] + (size_t)(CHUNK) * TBK * C::EB, &lds_b[ST][(wave * C::B_DMA + j) * 1024]); \
+    } while (0)
+
+    YV_TILE_ISSUE(0, 0);
+    if (C::NST == 3 && nks > 1) YV_TILE_ISSUE(1, 1);
+    int st = 0;
+    for (int c = 0; c < nks; ++c) {
+        // this wavefront's loads of chunk c have landed (the next chunk's may be in flight) ...
+        if (C::NST == 3 && c + 1 < nks) __builtin_amdgcn_s_waitcnt(vmcnt_only(C::NPW));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+        // ... and after the barrier every wavefront's have, and all reads of chunk c - 1 are
+        // done, so its stage can take chunk c + NST - 1
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        if (c + C::NST - 1 < nks) {
+            int sn = st + C::NST - 1;
+            if (sn >= C::NST) sn -= C::NST;
+            YV_TILE_ISSUE(c + C::NST - 1, sn);
+        }
+        const unsigned char* As = lds_a[st];
+        const unsigned char* Bs = lds_b[st];
+        bf16x8 bq[2][2];
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            if constexpr (C::EB == 1) {
+                const u32x4 raw = *(const u32x4*)(Bs + b_rd0[nb]);
+                const float s = GROUPED ? lds_s[sblk[nb]][(c * TBK) / 128] : cs[nb];
+                Frag16 f;
+                BLoad<WF>::cvt(make_uint4(raw.x, raw.y, raw.z, raw.w), s, f);
+                bq[nb][0] = f.v[0];
+                bq[nb][1] = f.v[1];
+            } else {
+                bq[nb][0] = *(const bf16x8*)(Bs + b_rd0[nb]);
+                bq[nb][1] = *(const bf16x8*)(Bs + b_rd1[nb]);
+            }
+        }
+#pragma unroll
+        for (int mb = 0; mb < 16; ++mb) {
+            const bf16x8 a0 = *(const bf16x8*)(As + a_rd0 + mb * 16 * 128);
+            const bf16x8 a1 = *(const bf16x8*)(As + a_rd1 + mb * 16 * 128);
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bq[nb][0], acc[mb][nb], 0, 0, 0);
+                acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bq[nb][1], acc[mb][nb], 0, 0, 0);
+            }
+        }
+        if (++st == C::NST) st = 0;
+    }
+#undef YV_TILE_ISSUE
+
     // epilogue: lane holds rows 4*(l/16)+i of each 16-row block, column l%16 of each block
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) {
+    for (int mb = 0; mb < 16; ++mb) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int r = row0 + wr * 128 + mb * 16 + (lane >> 4) * 4 + i;
+            const int r = row0 + mb * 16 + (lane >> 4) * 4 + i;
             if (r >= seg_end) continue;
             if constexpr (SWIGLU) {
-#pragma unroll
-                for (int nb = 0; nb < 2; ++nb) {
-                    const int n = n0 + wc * 32 + nb * 16 + (lane & 15);
-                    const float g = round_bf16(acc[mb][nb][i]);
-                    const float u = round_bf16(acc[mb][nb + 2][i]);
-                    const float sgl = round_bf16(silu(g));
-                    ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(sgl * u);
-                }
+                const int n = n0 + wave * 16 + (lane & 15);
+                const float gt = round_bf16(acc[mb][0][i]);
+                const float up = round_bf16(acc[mb][1][i]);
+                const float sgl = round_bf16(silu(gt));
+                ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(sgl * up);
             } else {
 #pragma unroll
-                for (int nb = 0; nb < 4; ++nb) {
-                    const int n = n0 + wc * 64 + nb * 16 + (lane & 15);
+                for (int nb = 0; nb < 2; ++nb) {
+                    const int n = n0 + wave * 32 + nb * 16 + (lane & 15);
                     ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(acc[mb][nb][i]);
                 }
             }
@@ -1150,7 +1180,8 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     const int maxrb = (act == YVMOE_ACT_BF16 && N * k <= 32 * E) ? 1 : 4;
     // 256-row LDS-tiled form when experts hold many rows (prefill-like batches)
     const bool tiled = act == YVMOE_ACT_BF16 && N * k >= 64 * E && F % (TBN / 2) == 0 && H % TBN == 0 &&
-                       (w->format == YVMOE_W_INT8 || w->format == YVMOE_W_FP8 || w->format == YVMOE_W_BF16);
+                       (w->format == YVMOE_W_INT8 || w->format == YVMOE_W_BF16 ||
+                        (w->format == YVMOE_W_FP8 && H <= 8192 && F <= 8192));
     const int tile_rows = tiled ? TBM : 16 * maxrb;
     const int T = max_tiles(N, k, E, S, tile_rows);
     build_tiles_kernel<<<1, 512, 0, st>>>(routing->offsets, E, S, N, k, tile_rows, seg, tile_seg,
