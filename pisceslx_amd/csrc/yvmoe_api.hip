@@ -227,16 +227,29 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
                              ffn_ws(N, k, E, experts->num_shared, experts->ffn, act_dtype).bytes);
     void* y = (char*)logits + align_up((size_t)N * ld * 4, 256);
     float* partials = (float*)((char*)y + y_bytes(N, k, experts->num_shared, experts->hidden, act_dtype));
+    // Small batches: the fused routing kernel reduces the router's split-K partial sums itself
+    // and builds the expert GEMM tile table, so neither needs a launch of its own.
+    const bool small = N > 0 && N <= kSmallRouteTok;
+    const int ks = router_ksplit(N, E, act_dtype, router->hidden);
+    const bool split = small && ks > 1;
     if (N > 0) {
-        rc = router_gemm_launch(x, act_dtype, N, router, logits, ld, partials, st);
+        rc = router_gemm_launch(x, act_dtype, N, router, logits, ld, partials, st, !split);
         if (rc) return rc;
     }
+    const float* lsrc = split ? partials : logits;
     const bool need_pred = !router->fixed_shape_mode && router->dynamic_capacity;
-    rc = route_launch(logits, ld, need_pred ? logits + pad16(E) : nullptr, ld, N, router, -1,
-                      routing, ws, st);
+    const int S = experts->num_shared;
+    TileTable tiles{};
+    if (small)
+        tiles = ffn_tile_table(N, k, E, S, experts->ffn, act_dtype,
+                               ffn_tile_rows(act_dtype, N, k, E, experts->hidden, experts->ffn,
+                                             experts->format),
+                               ws);
+    rc = route_launch(lsrc, ld, need_pred ? lsrc + pad16(E) : nullptr, ld, N, router, -1, routing,
+                      ws, st, split ? ks : 1, (long long)N * ld, small ? &tiles : nullptr);
     if (rc) return rc;
     if (N == 0) return YVMOE_OK;
-    rc = expert_ffn_launch(x, act_dtype, N, k, experts, routing, y, ws, st);
+    rc = expert_ffn_launch(x, act_dtype, N, k, experts, routing, y, ws, st, small);
     if (rc) return rc;
     return combine_launch(y, act_dtype, N, experts->hidden, k, experts->num_shared, routing, mix,
                           skip, out, shared_out, st);

@@ -1135,7 +1135,7 @@ int gemm_dispatch(int act, int wf, GemmParams p, int ntiles_max, int ncb, int ks
 }  // namespace
 
 int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, float* out, int ld,
-                       float* partials, hipStream_t st) {
+                       float* partials, hipStream_t st, bool reduce) {
     GemmParams p{};
     p.A = x;
     p.lda = r->hidden;
@@ -1157,36 +1157,59 @@ int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, flo
     p.out = partials;
     p.split_stride = (long long)N * ld;
     int rc = gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), 1, ks, st, "router_gemm");
-    if (rc) return rc;
+    if (rc || !reduce) return rc;
     const long long n = (long long)N * ld;
     reduce_splits_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(partials, ks, n, n, out);
     YV_LAUNCH_CHECK("router_reduce");
     return YVMOE_OK;
 }
 
+int ffn_tile_rows(int act, int N, int k, int E, int H, int F, int wf) {
+    // 256-row LDS-tiled form when experts hold many rows (prefill-like batches)
+    const bool tiled = act == YVMOE_ACT_BF16 && N * k >= 64 * E && F % (TBN / 2) == 0 && H % TBN == 0 &&
+                       (wf == YVMOE_W_INT8 || wf == YVMOE_W_BF16 ||
+                        (wf == YVMOE_W_FP8 && H <= 8192 && F <= 8192));
+    if (tiled) return TBM;
+    // 16-row tiles (one MFMA row block per wave) when experts hold few rows (decode-like
+    // batches), 64-row tiles otherwise
+    return (act == YVMOE_ACT_BF16 && N * k <= 32 * E) ? 16 : 64;
+}
+
+TileTable ffn_tile_table(int N, int k, int E, int S, int F, int act, int tile_rows, char* ws) {
+    const RouteWs RL = route_ws(N, E, k);
+    const FfnWs FL = ffn_ws(N, k, E, S, F, act);
+    char* fws = ws + RL.bytes;
+    TileTable t;
+    t.seg = (int*)(fws + FL.seg);
+    t.tile_seg = (int*)(fws + FL.tile_seg);
+    t.tile_row0 = (int*)(fws + FL.tile_row0);
+    t.ntiles = (int*)(fws + FL.ntiles);
+    t.S = S;
+    t.tile_rows = tile_rows;
+    return t;
+}
+
 int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_weights* w,
-                      const yvmoe_routing* routing, void* y, char* ws, hipStream_t st) {
+                      const yvmoe_routing* routing, void* y, char* ws, hipStream_t st, bool tiles_ready) {
     const int E = w->num_routed, S = w->num_shared, H = w->hidden, F = w->ffn;
     const RouteWs RL = route_ws(N, E, k);
     const FfnWs FL = ffn_ws(N, k, E, S, F, act);
     char* fws = ws + RL.bytes;
-    int* seg = (int*)(fws + FL.seg);
-    int* tile_seg = (int*)(fws + FL.tile_seg);
-    int* tile_row0 = (int*)(fws + FL.tile_row0);
-    int* ntiles = (int*)(fws + FL.ntiles);
     void* hbuf = fws + FL.h;
-    // 16-row tiles (one MFMA row block per wave) when experts hold few rows (decode-like
-    // batches), 64-row tiles otherwise
-    const int maxrb = (act == YVMOE_ACT_BF16 && N * k <= 32 * E) ? 1 : 4;
-    // 256-row LDS-tiled form when experts hold many rows (prefill-like batches)
-    const bool tiled = act == YVMOE_ACT_BF16 && N * k >= 64 * E && F % (TBN / 2) == 0 && H % TBN == 0 &&
-                       (w->format == YVMOE_W_INT8 || w->format == YVMOE_W_BF16 ||
-                        (w->format == YVMOE_W_FP8 && H <= 8192 && F <= 8192));
-    const int tile_rows = tiled ? TBM : 16 * maxrb;
+    const int tile_rows = ffn_tile_rows(act, N, k, E, H, F, w->format);
+    const bool tiled = tile_rows == TBM;
+    const int maxrb = tile_rows == 16 ? 1 : 4;
+    const TileTable tt = ffn_tile_table(N, k, E, S, F, act, tile_rows, ws);
+    int* seg = tt.seg;
+    int* tile_seg = tt.tile_seg;
+    int* tile_row0 = tt.tile_row0;
+    int* ntiles = tt.ntiles;
     const int T = max_tiles(N, k, E, S, tile_rows);
-    build_tiles_kernel<<<1, 512, 0, st>>>(routing->offsets, E, S, N, k, tile_rows, seg, tile_seg,
-                                          tile_row0, ntiles);
-    YV_LAUNCH_CHECK("build_tiles");
+    if (!tiles_ready) {
+        build_tiles_kernel<<<1, 512, 0, st>>>(routing->offsets, E, S, N, k, tile_rows, seg, tile_seg,
+                                              tile_row0, ntiles);
+        YV_LAUNCH_CHECK("build_tiles");
+    }
     const int wf = w->format;
     GemmParams p{};
     p.tile_seg = tile_seg;

@@ -46,6 +46,11 @@ inline int router_ld(int E, int act) {
 
 // K splits of the router GEMM: enough work-groups to spread a small batch over the chip,
 // at least 128 of K per split (2 k-steps); partial sums are reduced in split order.
+// Batches of up to kSmallRouteTok tokens take the two-kernel small-batch routing path
+// (per-token top-k with the router's split-K reduction folded in, then everything else in
+// one work-group).
+constexpr int kSmallRouteTok = 256;
+
 inline int router_ksplit(int N, int E, int act, int H) {
     const int groups = ceil_div(router_ld(E, act), 64);
     const int wgs = ceil_div(N > 0 ? N : 1, 64) * groups;
@@ -67,7 +72,7 @@ inline int max_tiles(int N, int k, int E, int S, int tile_rows) {
 // Workspace layout. The routing region depends on (N, E, k) only, so yvmoe_route and
 // yvmoe_expert_ffn agree on it without knowing each other's arguments.
 struct RouteWs {
-    size_t topp, w0, allowed, blockhist, blockoff, blocksum, tok, bytes;
+    size_t topp, w0, allowed, blockhist, blockoff, blocksum, tok, score, bytes;
 };
 struct FfnWs {
     size_t seg, tile_seg, tile_row0, ntiles, h, bytes;
@@ -85,6 +90,7 @@ inline RouteWs route_ws(int N, int E, int k) {
     w.blockoff = o;  o = align_up(o + (size_t)nb * E * 4, 256);
     w.blocksum = o;  o = align_up(o + (size_t)nb * 4, 256);
     w.tok = o;       o = align_up(o + nk * 4 + 4, 256);
+    w.score = o;     o = align_up(o + (size_t)N * 4, 256);
     w.bytes = o;
     return w;
 }
@@ -111,15 +117,35 @@ inline size_t y_bytes(int N, int k, int S, int H, int act) {
 }
 
 // ---------------------------------------------------------------- launchers
-// routing (yvmoe_route.hip)
+// Tile table of the expert GEMMs (segments = E routed experts, then S shared experts of N
+// rows each; every segment cut into tile_rows-row tiles), in the FFN workspace region.
+struct TileTable {
+    int* seg;
+    int* tile_seg;
+    int* tile_row0;
+    int* ntiles;
+    int S;
+    int tile_rows;
+};
+
+// routing (yvmoe_route.hip). Logits (and predictor columns) are the in-order sum of ksplit
+// partial copies split_stride floats apart (ksplit = 1: plain logits). With tiles non-null
+// (small batches only) the tile table is built as well.
 int route_launch(const float* logits, int ld, const float* pred, int pred_ld, int N,
                  const yvmoe_router* r, int cap_override, yvmoe_routing* out, char* ws,
-                 hipStream_t st);
-// GEMMs and combine (yvmoe_gemm.hip)
+                 hipStream_t st, int ksplit = 1, long long split_stride = 0,
+                 const TileTable* tiles = nullptr);
+// GEMMs and combine (yvmoe_gemm.hip). With reduce = false the router GEMM leaves its split-K
+// partial sums in partials (when it splits) for the routing kernel to reduce.
 int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, float* out,
-                       int ld, float* partials, hipStream_t st);
+                       int ld, float* partials, hipStream_t st, bool reduce = true);
+// Rows per tile of the expert GEMMs for this batch and layer, and the tile table's location
+// in the workspace.
+int ffn_tile_rows(int act, int N, int k, int E, int H, int F, int wf);
+TileTable ffn_tile_table(int N, int k, int E, int S, int F, int act, int tile_rows, char* ws);
 int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_weights* w,
-                      const yvmoe_routing* routing, void* y, char* ws, hipStream_t st);
+                      const yvmoe_routing* routing, void* y, char* ws, hipStream_t st,
+                      bool tiles_ready = false);
 int combine_launch(const void* y, int act, int N, int H, int k, int S,
                    const yvmoe_routing* routing, const float* mix, const void* skip,
                    void* out, void* shared_out, hipStream_t st);

@@ -48,6 +48,127 @@ __device__ __forceinline__ bool better(float v1, int e1, float v2, int e2) {
     return v1 > v2 || (v1 == v2 && e1 < e2);
 }
 
+// Value of lane (l + o) % 16 of this lane's 16-lane row (DPP row_ror, a VALU move instead of
+// an LDS permute). A butterfly over o = 8, 4, 2, 1 with rotations combines the same operand
+// values as the xor butterfly: after the step with o, every partial is periodic with period
+// o, so lane l's rotation partner holds the same bits as its xor partner l ^ o. Sums and
+// maxima are therefore bit-identical to the xor form.
+template <int O>
+__device__ __forceinline__ int rot16(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, 0x120 + O, 0xf, 0xf, false);
+}
+template <int O>
+__device__ __forceinline__ float rot16(float v) {
+    return __int_as_float(rot16<O>(__float_as_int(v)));
+}
+#define YV_BFLY16(STEP) do { STEP(8); STEP(4); STEP(2); STEP(1); } while (0)
+
+// Softmax and top-k of one token by its 16 lanes (lane l holds experts l, l + 16, ...).
+// logit(e) returns the fp32 logit of expert e. Lane j < k ends with the j-th choice: expert
+// id, its probability and its first-softmax weight exp(p_j - p_0) / sum.
+template <int NV, typename LogitFn>
+__device__ __forceinline__ void topk_token(LogitFn logit, const float* __restrict__ bias, int l, int E,
+                                           int k, int& my_id, float& my_ts, float& my_w0) {
+    float z[NV];
+    float m = -__builtin_huge_valf();
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int e = l + kLanes * i;
+        z[i] = 0.0f;
+        if (e < E) {
+            float v = logit(e);
+            if (bias) v = v + bias[e];
+            z[i] = v;
+            if (v > m) m = v;
+        }
+    }
+#define YV_MAXSTEP(O)                    \
+    do {                                 \
+        const float mo = rot16<O>(m);    \
+        if (mo > m) m = mo;              \
+    } while (0)
+    YV_BFLY16(YV_MAXSTEP);
+#undef YV_MAXSTEP
+    float part = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int e = l + kLanes * i;
+        if (e < E) {
+            z[i] = yv_expf(z[i] - m);
+            part = part + z[i];
+        }
+    }
+#define YV_SUMSTEP(O) part = part + rot16<O>(part)
+    YV_BFLY16(YV_SUMSTEP);
+#undef YV_SUMSTEP
+#pragma unroll
+    for (int i = 0; i < NV; ++i) z[i] = z[i] / part;
+
+    // top-k by (p desc, index asc)
+    unsigned taken = 0u;
+    float e0 = 0.0f, ts0 = 0.0f, tot = 0.0f;
+    my_ts = 0.0f;
+    my_id = 0;
+    for (int j = 0; j < k; ++j) {
+        float bv = -1.0f;
+        int be = 0x7fffffff;
+        int bi = -1;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int e = l + kLanes * i;
+            if (e < E && !((taken >> i) & 1u) && better(z[i], e, bv, be)) {
+                bv = z[i];
+                be = e;
+                bi = i;
+            }
+        }
+#define YV_ARGSTEP(O)                         \
+    do {                                      \
+        const float ov = rot16<O>(bv);        \
+        const int oe = rot16<O>(be);          \
+        if (better(ov, oe, bv, be)) {         \
+            bv = ov;                          \
+            be = oe;                          \
+        }                                     \
+    } while (0)
+        YV_BFLY16(YV_ARGSTEP);
+#undef YV_ARGSTEP
+        if ((be % kLanes) == l && bi >= 0 && (l + kLanes * bi) == be) taken |= 1u << bi;
+        if (j == 0) ts0 = bv;
+        const float ej = yv_expf(bv - ts0);
+        tot = tot + ej;
+        if (l == j) {
+            my_ts = bv;
+            my_id = be;
+            e0 = ej;
+        }
+    }
+    my_w0 = e0 / tot;
+}
+
+// complexity_predictor of one token by its 16 lanes: sigmoid(w2 . relu(W1 x + b1) + b2)
+// (gate.py:930-936); hidden unit c of W1 x is the sum of pred_terms columns q * 64 + c.
+// The result is valid on lane 0.
+template <typename PredFn>
+__device__ __forceinline__ float predictor_token(PredFn predcol, int pred_terms, const float* __restrict__ b1,
+                                                 const float* __restrict__ w2, const float* __restrict__ b2,
+                                                 int l) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPredDim / kLanes; ++i) {
+        const int c = l + kLanes * i;
+        float hsum = 0.0f;
+        for (int q = 0; q < pred_terms; ++q) hsum = hsum + predcol(q * kPredDim + c);
+        hsum = hsum + b1[c];
+        hsum = hsum > 0.0f ? hsum : 0.0f;
+        acc = acc + w2[c] * hsum;
+    }
+#define YV_SUMSTEP(O) acc = acc + rot16<O>(acc)
+    YV_BFLY16(YV_SUMSTEP);
+#undef YV_SUMSTEP
+    return 1.0f / (1.0f + expf(-(acc + b2[0])));
+}
+
 // One block = 64 tokens, 16 lanes per token, all 64 tokens in one pass (1024 threads).
 template <int NV>
 __global__ __launch_bounds__(1024) void route_topk_kernel(
@@ -65,103 +186,24 @@ __global__ __launch_bounds__(1024) void route_topk_kernel(
     if (tid < kTokPerBlock) score[tid] = 0.0f;
     __syncthreads();
 
-    {
-        const int tl = g;
-        const int t = blockIdx.x * kTokPerBlock + tl;
-        if (t < N) {  // uniform across the 16 lanes of a token
-            float z[NV];
-            float m = -__builtin_huge_valf();
-#pragma unroll
-            for (int i = 0; i < NV; ++i) {
-                const int e = l + kLanes * i;
-                z[i] = 0.0f;
-                if (e < E) {
-                    float v = logits[(size_t)t * ld + e];
-                    if (bias) v = v + bias[e];
-                    z[i] = v;
-                    if (v > m) m = v;
-                }
-            }
-#pragma unroll
-            for (int o = kLanes / 2; o >= 1; o >>= 1) {
-                float mo = __shfl_xor(m, o, kLanes);
-                if (mo > m) m = mo;
-            }
-            float part = 0.0f;
-#pragma unroll
-            for (int i = 0; i < NV; ++i) {
-                const int e = l + kLanes * i;
-                if (e < E) {
-                    z[i] = yv_expf(z[i] - m);
-                    part = part + z[i];
-                }
-            }
-#pragma unroll
-            for (int o = kLanes / 2; o >= 1; o >>= 1) part = part + __shfl_xor(part, o, kLanes);
-#pragma unroll
-            for (int i = 0; i < NV; ++i) z[i] = z[i] / part;
-
-            // top-k by (p desc, index asc)
-            unsigned taken = 0u;
-            float my_ts = 0.0f, my_e0 = 0.0f, ts0 = 0.0f, tot = 0.0f;
-            int my_id = 0;
-            for (int j = 0; j < k; ++j) {
-                float bv = -1.0f;
-                int be = 0x7fffffff;
-                int bi = -1;
-#pragma unroll
-                for (int i = 0; i < NV; ++i) {
-                    const int e = l + kLanes * i;
-                    if (e < E && !((taken >> i) & 1u) && better(z[i], e, bv, be)) {
-                        bv = z[i];
-                        be = e;
-                        bi = i;
-                    }
-                }
-#pragma unroll
-                for (int o = kLanes / 2; o >= 1; o >>= 1) {
-                    float ov = __shfl_xor(bv, o, kLanes);
-                    int oe = __shfl_xor(be, o, kLanes);
-                    if (better(ov, oe, bv, be)) {
-                        bv = ov;
-                        be = oe;
-                    }
-                }
-                if ((be % kLanes) == l && bi >= 0 && (l + kLanes * bi) == be) taken |= 1u << bi;
-                if (j == 0) ts0 = bv;
-                const float ej = yv_expf(bv - ts0);
-                tot = tot + ej;
-                if (l == j) {
-                    my_ts = bv;
-                    my_id = be;
-                    my_e0 = ej;
-                }
-            }
-            if (l < k) {
-                const size_t s = (size_t)t * k + l;
-                idx_out[s] = (int64_t)my_id;
-                topp[s] = my_ts;
-                w0[s] = my_e0 / tot;
-                allowed[s] = 1;
-                atomicAdd(&hist[my_id], 1);
-            }
-            if (pred != nullptr) {
-                // complexity_predictor: sigmoid(w2 . relu(W1 x + b1) + b2)  (gate.py:930-936)
-                float acc = 0.0f;
-#pragma unroll
-                for (int i = 0; i < kPredDim / kLanes; ++i) {
-                    const int c = l + kLanes * i;
-                    float hsum = 0.0f;
-                    for (int q = 0; q < pred_terms; ++q)
-                        hsum = hsum + pred[(size_t)t * pred_ld + q * kPredDim + c];
-                    hsum = hsum + b1[c];
-                    hsum = hsum > 0.0f ? hsum : 0.0f;
-                    acc = acc + w2[c] * hsum;
-                }
-#pragma unroll
-                for (int o = kLanes / 2; o >= 1; o >>= 1) acc = acc + __shfl_xor(acc, o, kLanes);
-                if (l == 0) score[tl] = 1.0f / (1.0f + expf(-(acc + b2[0])));
-            }
+    const int tl = g;
+    const int t = blockIdx.x * kTokPerBlock + tl;
+    if (t < N) {  // uniform across the 16 lanes of a token
+        int my_id;
+        float my_ts, my_w0;
+        topk_token<NV>([&](int e) { return logits[(size_t)t * ld + e]; }, bias, l, E, k, my_id, my_ts, my_w0);
+        if (l < k) {
+            const size_t s = (size_t)t * k + l;
+            idx_out[s] = (int64_t)my_id;
+            topp[s] = my_ts;
+            w0[s] = my_w0;
+            allowed[s] = 1;
+            atomicAdd(&hist[my_id], 1);
+        }
+        if (pred != nullptr) {
+            const float sc = predictor_token([&](int c) { return pred[(size_t)t * pred_ld + c]; },
+                                             pred_terms, b1, w2, b2, l);
+            if (l == 0) score[tl] = sc;
         }
     }
     __syncthreads();
@@ -418,6 +460,307 @@ __global__ __launch_bounds__(256) void renorm_kernel(const float* __restrict__ w
     for (int j = 0; j < k; ++j) w[(size_t)t * k + j] = (tmp[j] * keep) / den;
 }
 
+// ------------------------------------------------------------------ small batches
+// Routing of a batch of up to kSmallRouteTok tokens (decode) in two launches.
+//
+// route_topk_small_kernel: 4 tokens per work-group (16 lanes each). The token's logits and
+// predictor columns are first summed over the router GEMM's K splits, in split order (the
+// order of reduce_splits_kernel), into LDS with all loads in flight; then the per-token
+// top-k and predictor run from LDS (topk_token, predictor_token: the same code as the
+// multi-block path).
+//
+// route_small_kernel: one work-group of 1024 threads for the rest: histogram, scan and
+// capacity (the fixed-order complexity sums of the multi-block path: per 64-token block in
+// token order, then the same 1024-wide tree), the stable scatter, the capacity trim, the
+// renormalisation, and the expert GEMM tile table. The trim ranks the slots of an over-full
+// expert by (p desc, token asc) directly, which keeps the same set as the radix select of
+// capacity_trim_kernel (p > T, then the first ties in token order).
+constexpr int kSmallSlots = kSmallRouteTok * YVMOE_MAX_TOPK;
+constexpr int kSmallChunks = kSmallSlots / 64;
+constexpr int kSmallBlocks = kSmallRouteTok / kTokPerBlock;
+constexpr int kMaxPredTerms = 3;  // predictor columns per hidden unit held in LDS
+
+// One token per work-group of 256 threads: each thread reduces about one column over the K
+// splits (all split loads of a column in flight together), then the token's 16 lanes run
+// the top-k and the predictor from LDS.
+template <int NV>
+__global__ __launch_bounds__(256) void route_topk_small_kernel(
+    const float* __restrict__ logits, const float* __restrict__ pred, int ld, int ksplit,
+    long long split_stride, int pred_terms, const float* __restrict__ bias, const float* __restrict__ b1,
+    const float* __restrict__ w2, const float* __restrict__ b2, int N, int E, int k,
+    int64_t* __restrict__ idx_out, float* __restrict__ topp, float* __restrict__ w0,
+    float* __restrict__ score) {
+    __shared__ float s_lg[16 * NV];
+    __shared__ float s_pr[kMaxPredTerms * kPredDim];
+    const int tid = threadIdx.x;
+    const int t = blockIdx.x;
+    const int npc = (pred != nullptr) ? pred_terms * kPredDim : 0;
+    for (int c = tid; c < E + npc; c += 256) {
+        const float* base = (c < E) ? logits + (size_t)t * ld + c : pred + (size_t)t * ld + (c - E);
+        // unconditional loads (split index clamped): no branch, so all are in flight together
+        float part[16];
+#pragma unroll
+        for (int z = 0; z < 16; ++z) part[z] = base[(size_t)min(z, ksplit - 1) * split_stride];
+        float v = part[0];
+#pragma unroll
+        for (int z = 1; z < 16; ++z) v = (z < ksplit) ? v + part[z] : v;
+        for (int z = 16; z < ksplit; ++z) v = v + base[(size_t)z * split_stride];
+        if (c < E) s_lg[c] = v;
+        else s_pr[c - E] = v;
+    }
+    __syncthreads();
+    if (tid >= kLanes) return;  // no barrier follows
+    const int l = tid;
+    int my_id;
+    float my_ts, my_w0;
+    topk_token<NV>([&](int e) { return s_lg[e]; }, bias, l, E, k, my_id, my_ts, my_w0);
+    if (l < k) {
+        const size_t s = (size_t)t * k + l;
+        idx_out[s] = (int64_t)my_id;
+        topp[s] = my_ts;
+        w0[s] = my_w0;
+    }
+    if (pred != nullptr) {
+        const float sv = predictor_token([&](int c) { return s_pr[c]; }, pred_terms, b1, w2, b2, l);
+        if (l == 0) score[t] = sv;
+    }
+}
+
+struct SmallRouteArgs {
+    int N, E, k;
+    int cap_mode, cap_explicit, min_cap;
+    double cap_factor;
+    const int64_t* indices;
+    const float* topp;
+    const float* w0;
+    const float* score;
+    float* weights;
+    int* counts;
+    int* offsets;
+    int* perm;
+    int* pos;
+    int* cap_out;
+    int* tok;
+    TileTable tiles;  // tiles.seg == nullptr: no tile table
+};
+
+// Inclusive prefix sum over the 64 lanes of a wavefront.
+__device__ __forceinline__ int wave_incl_scan(int v) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int u = __shfl_up(v, o, 64);
+        if (lane >= o) v += u;
+    }
+    return v;
+}
+
+__global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
+    __shared__ int hist[YVMOE_MAX_EXPERTS];
+    __shared__ int s_off[YVMOE_MAX_EXPERTS + 1];
+    __shared__ unsigned short cnt[kSmallChunks][YVMOE_MAX_EXPERTS];
+    __shared__ unsigned char s_idx[kSmallSlots];
+    __shared__ unsigned char s_allowed[kSmallSlots];
+    __shared__ unsigned short s_rk[kSmallSlots];
+    __shared__ unsigned short s_perm[kSmallSlots];
+    __shared__ float s_topp[kSmallSlots];
+    __shared__ float s_score[kSmallRouteTok];
+    __shared__ int s_cap;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int N = a.N, E = a.E, k = a.k;
+    const int nb = (N + kTokPerBlock - 1) / kTokPerBlock;
+    const int nslots = N * k;
+    const int nchunks = (nslots + 63) / 64;
+
+    for (int q = tid; q < E; q += 1024) hist[q] = 0;
+    for (int q = tid; q < nchunks * E; q += 1024) cnt[q / E][q % E] = 0;
+    __syncthreads();
+    for (int s = tid; s < nslots; s += 1024) {
+        const int e = (int)a.indices[s];
+        s_idx[s] = (unsigned char)e;
+        s_topp[s] = a.topp[s];
+        s_allowed[s] = 1;
+        atomicAdd(&hist[e], 1);
+    }
+    if (a.cap_mode == 2 && tid < kSmallRouteTok) s_score[tid] = tid < N ? a.score[tid] : 0.0f;
+    __syncthreads();
+
+    // stable scatter, part 1: rank within a 64-slot chunk from 8 ballots over the expert id
+    // bits (all waves); counts, offsets and capacity (wave 0, after its chunks)
+    for (int c = wave; c < nchunks; c += 16) {
+        const int s = c * 64 + lane;
+        const bool valid = s < nslots;
+        const int e = valid ? (int)s_idx[s] : 0;
+        unsigned long long mask = __ballot(valid);
+#pragma unroll
+        for (int bit = 0; bit < 8; ++bit) {
+            const bool on = (e >> bit) & 1;
+            const unsigned long long bb = __ballot(valid && on);
+            mask &= on ? bb : ~bb;
+        }
+        const unsigned long long below = mask & ((1ull << lane) - 1ull);
+        if (valid) {
+            s_rk[s] = (unsigned short)__popcll(below);
+            if (below == 0ull) cnt[c][e] = (unsigned short)__popcll(mask);
+        }
+    }
+    if (wave == 0) {
+        // lane l owns experts 4l .. 4l + 3 (E <= 256)
+        int h[4], loc = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = 4 * lane + i;
+            h[i] = e < E ? hist[e] : 0;
+            loc += h[i];
+        }
+        int run = wave_incl_scan(loc) - loc;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int e = 4 * lane + i;
+            if (e < E) {
+                a.counts[e] = h[i];
+                run += h[i];
+                a.offsets[e + 1] = run;
+                s_off[e + 1] = run;
+            }
+        }
+        if (lane == 0) {
+            a.offsets[0] = 0;
+            s_off[0] = 0;
+            // complexity sums: per 64-token block in token order (invalid tokens 0), then
+            // route_scan_kernel's 1024-wide tree, which for nb <= 4 block sums r0..r3 (the
+            // rest 0) reduces to (r0 + r2) + (r1 + r3)
+            float r[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (a.cap_mode == 2)
+                for (int b = 0; b < nb; ++b) {
+                    float bs = 0.0f;
+                    for (int i = 0; i < kTokPerBlock; ++i) bs = bs + s_score[b * kTokPerBlock + i];
+                    r[b] = 0.0f + bs;
+                }
+            const float total = (r[0] + r[2]) + (r[1] + r[3]);
+            int cap = -1;
+            if (a.cap_mode == 1) {
+                cap = a.cap_explicit;
+            } else if (a.cap_mode == 2 || a.cap_mode == 3) {
+                double cf = a.cap_factor;
+                if (a.cap_mode == 2) {
+                    const float avg = total / (float)N;  // complexity_scores.mean() (gate.py:1117)
+                    cf = 0.5 + 1.5 * (double)avg;
+                    if (cf > 2.0) cf = 2.0;
+                    if (cf < 0.5) cf = 0.5;
+                }
+                cap = (int)((double)N * cf / (double)E);
+                if (cap < a.min_cap) cap = a.min_cap;
+            }
+            *a.cap_out = cap;
+            s_cap = cap;
+        }
+    }
+    __syncthreads();
+
+    // stable scatter, part 2: chunk counts prefix-summed per expert, then positions
+    if (tid < E) {
+        int run = 0;
+        for (int c = 0; c < nchunks; ++c) {
+            const int v = cnt[c][tid];
+            cnt[c][tid] = (unsigned short)run;
+            run += v;
+        }
+    }
+    __syncthreads();
+    for (int s = tid; s < nslots; s += 1024) {
+        const int e = s_idx[s];
+        const int p = s_off[e] + cnt[s / 64][e] + s_rk[s];
+        a.perm[p] = s;
+        a.pos[s] = p;
+        a.tok[p] = s / k;
+        s_perm[p] = (unsigned short)s;
+    }
+    __syncthreads();
+
+    // capacity trim: a wavefront per over-full expert; slot i (token order) is kept iff
+    // #{j: p_j > p_i} + #{j < i: p_j == p_i} < cap. The last wave builds the tile table.
+    const int cap = s_cap;
+    if (cap >= 0) {
+        for (int e = wave; e < E; e += 15) {
+            if (wave == 15) break;
+            const int n = s_off[e + 1] - s_off[e];
+            if (n <= cap) continue;
+            const int off = s_off[e];
+            for (int i = lane; i < n; i += 64) {
+                const int si = s_perm[off + i];
+                const float pi = s_topp[si];
+                int rank = 0;
+                for (int j = 0; j < n; ++j) {
+                    const float pj = s_topp[s_perm[off + j]];
+                    rank += (pj > pi || (pj == pi && j < i)) ? 1 : 0;
+                }
+                if (rank >= cap) s_allowed[si] = 0;
+            }
+        }
+    }
+    if (wave == 15 && a.tiles.seg != nullptr) {
+        // tile table of the expert GEMMs (build_tiles_kernel): lane l owns segments 5l .. 5l + 4
+        const int S = a.tiles.S, tr = a.tiles.tile_rows;
+        const int nseg = E + S;
+        int s0[5], nt[5], loc = 0;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            const int sg = 5 * lane + i;
+            int b = 0, e_ = 0;
+            if (sg < nseg) {
+                if (sg < E) {
+                    b = s_off[sg];
+                    e_ = s_off[sg + 1];
+                } else {
+                    b = N * k + (sg - E) * N;
+                    e_ = b + N;
+                }
+                a.tiles.seg[sg] = b;
+                if (sg == nseg - 1) a.tiles.seg[nseg] = e_;
+            }
+            s0[i] = b;
+            nt[i] = (e_ - b + tr - 1) / tr;
+            loc += nt[i];
+        }
+        const int incl = wave_incl_scan(loc);
+        int start = incl - loc;
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            const int sg = 5 * lane + i;
+            for (int q = 0; q < nt[i]; ++q) {
+                a.tiles.tile_seg[start + q] = sg;
+                a.tiles.tile_row0[start + q] = s0[i] + q * tr;
+            }
+            start += nt[i];
+        }
+        if (lane == 63) *a.tiles.ntiles = incl;
+    }
+    __syncthreads();
+
+    // weights: renormalised over the kept slots (renorm_kernel), or the first softmax
+    // unchanged in fixed-shape mode
+    if (tid < N) {
+        const int t = tid;
+        if (a.cap_mode != 0) {
+            float tmp[YVMOE_MAX_TOPK];
+            float tot = 0.0f;
+            for (int j = 0; j < k; ++j) {
+                const int s = t * k + j;
+                tmp[j] = a.w0[s] * (s_allowed[s] ? 1.0f : 0.0f);
+                tot = tot + tmp[j];
+            }
+            const float den = tot > 1e-8f ? tot : 1e-8f;
+            const float keep = tot > 0.0f ? 1.0f : 0.0f;
+            for (int j = 0; j < k; ++j) a.weights[t * k + j] = (tmp[j] * keep) / den;
+        } else {
+            for (int j = 0; j < k; ++j) a.weights[t * k + j] = a.w0[t * k + j];
+        }
+    }
+}
+
 __global__ void copy_f32_kernel(const float* __restrict__ a, float* __restrict__ b, int n) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) b[i] = a[i];
@@ -427,7 +770,7 @@ __global__ void copy_f32_kernel(const float* __restrict__ a, float* __restrict__
 
 int route_launch(const float* logits, int ld, const float* pred, int pred_ld, int N,
                  const yvmoe_router* r, int cap_override, yvmoe_routing* out, char* ws,
-                 hipStream_t st) {
+                 hipStream_t st, int ksplit, long long split_stride, const TileTable* tiles) {
     const int E = r->num_experts, k = r->top_k;
     const RouteWs L = route_ws(N, E, k);
     float* topp = (float*)(ws + L.topp);
@@ -445,6 +788,45 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
     YV_REQUIRE(cap_mode != 2 || pred != nullptr, YVMOE_ERR_ARG,
                "dynamic capacity needs the complexity predictor columns (or a capacity override)");
     const int pred_terms = (pred_ld - pad16(E)) / kPredDim;
+    if (N > 0 && N <= kSmallRouteTok && (use_pred == nullptr || pred_terms <= kMaxPredTerms)) {
+        float* score = (float*)(ws + L.score);
+        const float* lpred = use_pred;
+#define YV_TOPKS(NVV)                                                                              \
+    route_topk_small_kernel<NVV><<<N, 256, 0, st>>>(                                                \
+        logits, lpred, ld, ksplit, split_stride, pred_terms, r->bias, r->b1, r->w2, r->b2, N, E, k, \
+        out->indices, topp, w0, score)
+        if (E <= 16) YV_TOPKS(1);
+        else if (E <= 64) YV_TOPKS(4);
+        else if (E <= 128) YV_TOPKS(8);
+        else YV_TOPKS(16);
+#undef YV_TOPKS
+        YV_LAUNCH_CHECK("route_topk_small");
+        SmallRouteArgs a{};
+        a.N = N;
+        a.E = E;
+        a.k = k;
+        a.cap_mode = cap_mode;
+        a.cap_explicit = cap_override;
+        a.min_cap = r->min_capacity;
+        a.cap_factor = r->capacity_factor;
+        a.indices = out->indices;
+        a.topp = topp;
+        a.w0 = w0;
+        a.score = score;
+        a.weights = out->weights;
+        a.counts = out->counts;
+        a.offsets = out->offsets;
+        a.perm = out->perm;
+        a.pos = out->pos;
+        a.cap_out = out->capacity;
+        a.tok = tok;
+        if (tiles) a.tiles = *tiles;
+        route_small_kernel<<<1, 1024, 0, st>>>(a);
+        YV_LAUNCH_CHECK("route_small");
+        return YVMOE_OK;
+    }
+    YV_REQUIRE(ksplit == 1 && tiles == nullptr, YVMOE_ERR_ARG,
+               "internal: split logits and tile building are for small batches only");
     if (N == 0) {
         route_scan_kernel<<<1, 1024, 0, st>>>(blockhist, 0, E, 0, blocksum, cap_mode,
                                                 cap_override, r->min_capacity,

@@ -96,3 +96,36 @@ def test_route_deterministic(cuda, oracle):
     b = yvf.route(logits, st, predictor=False, capacity_override=300)
     for x, y in ((a.perm, b.perm), (a.weights, b.weights), (a.pos, b.pos)):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("N,E,k,cap", [
+    (256, 64, 6, 3),        # largest batch of the single-work-group path
+    (257, 64, 6, 3),        # smallest batch of the multi-block path
+    (200, 8, 2, 5),
+    (129, 256, 16, 1),
+    (64, 64, 6, 0),
+])
+def test_route_small_batch_boundary(cuda, oracle, N, E, k, cap):
+    rng = np.random.default_rng(N * 13 + E)
+    logits = (rng.standard_normal((N, E)) * 1.7).astype(np.float32)
+    _check(oracle, logits, k, cap)
+
+
+@pytest.mark.parametrize("E,k,cap", [(8, 2, 5), (64, 6, 3), (256, 8, 2)])
+def test_route_small_batch_ties(cuda, oracle, E, k, cap):
+    rng = np.random.default_rng(E * 3 + k)
+    logits = rng.integers(-1, 2, size=(200, E)).astype(np.float32)
+    _check(oracle, logits, k, cap)
+
+
+def test_route_small_batch_one_expert_and_fixed(cuda, oracle):
+    rng = np.random.default_rng(6)
+    N, E, k = 200, 16, 2
+    logits = (rng.standard_normal((N, E)) * 0.1).astype(np.float32)
+    logits[:, 3] += 20.0
+    for cap in (0, 1, 17, 199, 200):
+        _check(oracle, logits, k, cap)
+    E, k, N = 256, 8, 128
+    bias = zipf_bias(E, 1.2, 16, 0)
+    logits = (rng.standard_normal((N, E)) * 1.7).astype(np.float32)
+    _check(oracle, logits, k, -1, bias)
