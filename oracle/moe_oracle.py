@@ -13,7 +13,9 @@ It restates the reference algorithm on the CPU with torch ops, following:
 * ``PiscesLxFusedMoEDispatch.forward`` opss/infer/fused_moe.py:54-123 — stable argsort,
   bincount offsets, a loop over active experts, then the weighted combine;
 * ``YvSwiGLUExpert.forward`` model/moe/expert.py:475-489 — ``down(silu(gate(x)) * up(x))``
-  with ``F.linear`` in the layer dtype (fp32 or bf16) on weights dequantized inside the
+  with every ``F.linear`` correctly rounded to the layer dtype (exact float64 sum, one
+  rounding; the reference's fp32 accumulation order is BLAS-dependent, so this is the
+  order-free statement of the same rounding points), on weights dequantized inside the
   expert loop (bounded host memory);
 * ``_compute_shared_expert_output`` model/moe/layer.py:812-865 — fused gate/up
   projection, ``softmax(shared_expert_weight)`` mixture;
@@ -202,9 +204,17 @@ def layer_capacity(params: LayerParams, x2d: torch.Tensor) -> int:
     return max(c, params.min_capacity)
 
 
+def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """F.linear(x, w) of the layer dtype, correctly rounded: the exact (float64) sum rounded
+    once to x's dtype. The reference's F.linear accumulates in fp32 in a BLAS-dependent
+    order; the correctly rounded product is the order-free statement of the same rounding
+    point, so any fp32 implementation differs from it only by its own accumulation error."""
+    return (x.double() @ w.double().t()).to(x.dtype)
+
+
 def swiglu(xs: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, wd: torch.Tensor) -> torch.Tensor:
     """YvSwiGLUExpert.forward (expert.py:484-489) in the dtype of its inputs."""
-    return F.linear(F.silu(F.linear(xs, wg)) * F.linear(xs, wu), wd)
+    return linear(F.silu(linear(xs, wg)) * linear(xs, wu), wd)
 
 
 def layer_forward(x2d: torch.Tensor, params: LayerParams, logits: Optional[np.ndarray] = None,
@@ -266,8 +276,8 @@ def layer_forward(x2d: torch.Tensor, params: LayerParams, logits: Optional[np.nd
         for s in range(S):
             wg, wu, wd = params.expert(E + s)
             wf = torch.cat([wg, wu], dim=0).to(dtype)  # layer.py:844 fused gate/up
-            g, u = F.linear(x2d[rows], wf).chunk(2, dim=-1)
-            so = F.linear(F.silu(g) * u, wd.to(dtype))
+            g, u = linear(x2d[rows], wf).chunk(2, dim=-1)
+            so = linear(F.silu(g) * u, wd.to(dtype))
             shared[rows] = shared[rows] + mix[s].to(dtype) * so
         out = out + shared
         if skip is not None and tuple(skip.shape) == (N, H):

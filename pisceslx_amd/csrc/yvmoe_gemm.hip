@@ -28,6 +28,13 @@
 
 #include "yvmoe_internal.h"
 
+#ifndef YV_NB1
+#define YV_NB1 1  // column blocks per wavefront, streaming gate/up (1 measured best)
+#endif
+#ifndef YV_NB2
+#define YV_NB2 1  // column blocks per wavefront, streaming down projection (1 measured best)
+#endif
+
 namespace yvmoe {
 namespace {
 
@@ -384,14 +391,16 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
 // ------------------------------------------------------------------ bf16, streaming form
 // Weight-streaming form for batches whose experts hold few rows (decode). A work-group of 4
 // wavefronts owns one tile (up to 16*MAXRB rows of one expert); every wavefront streams one
-// weight matrix over one 16-column block: for the down projection 4 blocks per work-group,
-// for gate/up 2 column blocks with a gate wavefront and an up wavefront each, which swap
-// accumulators through LDS for the SwiGLU epilogue. The K loop runs in chunks of U k-steps:
-// the work-group stages the chunk's activation rows once in LDS (double-buffered, rows
-// padded by 16 bytes so the 16 row-lanes of a fragment read hit distinct banks), and each
-// wavefront loads only its weights from HBM, in plain load-then-use batches (the pattern
-// that measured closest to the HBM ceiling), reading activation fragments from LDS.
-template <int WF, int EPI, int U, int MAXRB>
+// weight matrix over NB 16-column blocks: for the down projection 4 x NB blocks per
+// work-group, for gate/up 2 x NB column blocks with a gate wavefront and an up wavefront each,
+// which swap accumulators through LDS for the SwiGLU epilogue. The K loop runs in chunks of U
+// k-steps: the work-group stages the chunk's activation rows once in LDS (double-buffered,
+// rows padded by 16 bytes so the 16 row-lanes of a fragment read hit distinct banks), and
+// each wavefront loads only its weights from HBM, in plain load-then-use batches (the pattern
+// that measured closest to the HBM ceiling), reading activation fragments from LDS. More
+// column blocks per wavefront put more weight bytes in flight per activation chunk and per
+// barrier.
+template <int WF, int EPI, int U, int MAXRB, int NB>
 __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int cgroup,
                                             uint4 (&As)[2][16 * MAXRB * (U * 8 + 1)]) {
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
@@ -401,7 +410,7 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
     constexpr int CHUNK_U4 = ROWS * U * 8;       // uint4 of one chunk
     constexpr int PER_THREAD = CHUNK_U4 / 256;   // uint4 each thread stages per chunk
     static_assert(CHUNK_U4 % 256 == 0, "chunk must split evenly over 256 threads");
-    static_assert(2 * ROWS * ROW_U4 * 16 >= 2 * 64 * MAXRB * 16, "LDS too small for the swap");
+    static_assert(2 * ROWS * ROW_U4 * 16 >= 2 * 64 * MAXRB * NB * 16, "LDS too small for the swap");
     typedef BLoad<WF> BL;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -412,9 +421,8 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
     const int nvalid = min(ROWS, seg_end - row0);
     const int nrb = (nvalid + 15) / 16;
     const int mat = SWIGLU ? (wave & 1) : 0;  // 0: gate (or down), 1: up
-    const int col0 = SWIGLU ? (cgroup * 2 + (wave >> 1)) * 16 : (cgroup * 4 + wave) * 16;
-    const bool active = col0 < p.ncols;  // waves past the last column still stage and sync
-    const int n = min(col0, p.ncols - 16) + (lane & 15);
+    // first column of block b of this wavefront
+    const int colw = SWIGLU ? (cgroup * 2 + (wave >> 1)) * 16 * NB : (cgroup * 4 + wave) * 16 * NB;
     const int kl = (lane >> 4) * 16;
     const int nks = p.K / 64;
     const int nchunks = (nks + U - 1) / U;
@@ -447,12 +455,24 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
     const long long e_off = (long long)e * p.b_stride;
     const long long s_off = (long long)e * p.s_stride;
     const void* S = mat ? p.S1 : p.S0;
-    const char* bptr = BL::ptr(mat ? p.B1 : p.B0, e_off, n, p.K, kl);
-    const float scl = b_scale<WF>(S, s_off, n, p.K, 0);
-
-    f32x4 acc[MAXRB];
+    bool active[NB];
+    int n[NB];
+    const char* bptr[NB];
+    float scl[NB];
 #pragma unroll
-    for (int rb = 0; rb < MAXRB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < NB; ++b) {
+        const int c0 = colw + b * 16;
+        active[b] = c0 < p.ncols;  // blocks past the last column still stage and sync
+        n[b] = min(c0, p.ncols - 16) + (lane & 15);
+        bptr[b] = BL::ptr(mat ? p.B1 : p.B0, e_off, n[b], p.K, kl);
+        scl[b] = b_scale<WF>(S, s_off, n[b], p.K, 0);
+    }
+
+    f32x4 acc[NB][MAXRB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int rb = 0; rb < MAXRB; ++rb) acc[b][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     {
         uint4 v[PER_THREAD];
@@ -462,34 +482,45 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
     __syncthreads();
     for (int c = 0; c < nchunks; ++c) {
         const int ks0 = c * U;
-        typename BL::Raw bw[U];
-        float sg[U];
-        if (active) {
+        typename BL::Raw bw[NB][U];
+        float sg[NB][U];
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int ks = min(ks0 + u, nks - 1);
-                BL::load(bw[u], bptr, ks * 64);
-                if constexpr (GROUPED) sg[u] = b_scale<WF>(S, s_off, n, p.K, ks * 64);
-                else sg[u] = scl;
+        for (int b = 0; b < NB; ++b) {
+            if (active[b]) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int ks = min(ks0 + u, nks - 1);
+                    BL::load(bw[b][u], bptr[b], ks * 64);
+                    if constexpr (GROUPED) sg[b][u] = b_scale<WF>(S, s_off, n[b], p.K, ks * 64);
+                    else sg[b][u] = scl[b];
+                }
             }
         }
         uint4 nxt[PER_THREAD];
         if (c + 1 < nchunks) stage_load(c + 1, nxt);
-        if (active) {
-            const uint4* arow = &As[c & 1][(lane & 15) * ROW_U4 + (lane >> 4) * 2];
+        const uint4* arow = &As[c & 1][(lane & 15) * ROW_U4 + (lane >> 4) * 2];
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                if (ks0 + u < nks) {
-                    Frag16 bf;
-                    BL::cvt(bw[u], sg[u], bf);
+        for (int u = 0; u < U; ++u) {
+            if (ks0 + u < nks) {
+                Frag16 af[MAXRB];
 #pragma unroll
-                    for (int rb = 0; rb < MAXRB; ++rb) {
-                        if (rb < nrb) {
-                            Frag16 af;
-                            af.u[0] = arow[rb * 16 * ROW_U4 + u * 8];
-                            af.u[1] = arow[rb * 16 * ROW_U4 + u * 8 + 1];
-                            acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af.v[0], bf.v[0], acc[rb], 0, 0, 0);
-                            acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af.v[1], bf.v[1], acc[rb], 0, 0, 0);
+                for (int rb = 0; rb < MAXRB; ++rb) {
+                    if (rb < nrb) {
+                        af[rb].u[0] = arow[rb * 16 * ROW_U4 + u * 8];
+                        af[rb].u[1] = arow[rb * 16 * ROW_U4 + u * 8 + 1];
+                    }
+                }
+#pragma unroll
+                for (int b = 0; b < NB; ++b) {
+                    if (active[b]) {
+                        Frag16 bf;
+                        BL::cvt(bw[b][u], sg[b][u], bf);
+#pragma unroll
+                        for (int rb = 0; rb < MAXRB; ++rb) {
+                            if (rb < nrb) {
+                                acc[b][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[rb].v[0], bf.v[0], acc[b][rb], 0, 0, 0);
+                                acc[b][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[rb].v[1], bf.v[1], acc[b][rb], 0, 0, 0);
+                            }
                         }
                     }
                 }
@@ -502,56 +533,73 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
     if constexpr (SWIGLU) {
         // up wavefronts hand their accumulators to the gate wavefront of the same columns
         float* xchg = (float*)&As[0][0];
+        auto xi = [&](int b, int rb, int i) { return ((((wave >> 1) * NB + b) * MAXRB + rb) * 4 + i) * 64 + lane; };
         if (mat == 1) {
 #pragma unroll
-            for (int rb = 0; rb < MAXRB; ++rb)
+            for (int b = 0; b < NB; ++b)
 #pragma unroll
-                for (int i = 0; i < 4; ++i) xchg[(((wave >> 1) * MAXRB + rb) * 4 + i) * 64 + lane] = acc[rb][i];
+                for (int rb = 0; rb < MAXRB; ++rb)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) xchg[xi(b, rb, i)] = acc[b][rb][i];
         }
         __syncthreads();
-        if (mat == 0 && active) {
+        if (mat == 0) {
 #pragma unroll
-        for (int rb = 0; rb < MAXRB; ++rb) {
-            if (rb < nrb) {
+            for (int b = 0; b < NB; ++b) {
+                if (!active[b]) continue;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = row0 + rb * 16 + (lane >> 4) * 4 + i;
-                    if (r < seg_end) {
-                        const float g = round_bf16(acc[rb][i]);
-                        const float u = round_bf16(xchg[(((wave >> 1) * MAXRB + rb) * 4 + i) * 64 + lane]);
-                        const float sgl = round_bf16(silu(g));
-                        ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(sgl * u);
+                for (int rb = 0; rb < MAXRB; ++rb) {
+                    if (rb < nrb) {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int r = row0 + rb * 16 + (lane >> 4) * 4 + i;
+                            if (r < seg_end) {
+                                const float g = round_bf16(acc[b][rb][i]);
+                                const float u = round_bf16(xchg[xi(b, rb, i)]);
+                                const float sgl = round_bf16(silu(g));
+                                ((unsigned short*)p.out)[(long long)r * p.ldo + n[b]] = f32_to_bf16_rne(sgl * u);
+                            }
+                        }
                     }
                 }
             }
         }
-        }
         __syncthreads();  // the exchange area is the next item's staging buffer
     } else {
-        if (!active) return;
 #pragma unroll
-        for (int rb = 0; rb < MAXRB; ++rb) {
-            if (rb < nrb) {
+        for (int b = 0; b < NB; ++b) {
+            if (!active[b]) continue;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int r = row0 + rb * 16 + (lane >> 4) * 4 + i;
-                    if (r < seg_end)
-                        ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(acc[rb][i]);
+            for (int rb = 0; rb < MAXRB; ++rb) {
+                if (rb < nrb) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int r = row0 + rb * 16 + (lane >> 4) * 4 + i;
+                        if (r < seg_end)
+                            ((unsigned short*)p.out)[(long long)r * p.ldo + n[b]] = f32_to_bf16_rne(acc[b][rb][i]);
+                    }
                 }
             }
         }
     }
 }
 
-// Persistent launch: work-group b processes items b, b + G, ... of the ntiles x ngroups
-// (tile fastest) item space, with G chosen by the host so each does the same count.
-template <int WF, int EPI, int U, int MAXRB>
+// One item of the ntiles x ngroups item space (tile fastest) per work-group. Consecutive
+// work-group ids go to different XCDs (round-robin dispatch), so the item space is cut into 8
+// contiguous ranges, one per XCD: the tiles that share weights (the 16-row tiles of a shared
+// expert, which all read the same columns) then run together on one XCD and fetch those
+// weights from HBM once into its L2 instead of once per tile.
+template <int WF, int EPI, int U, int MAXRB, int NB>
 __global__ __launch_bounds__(256) void gemm_stream_kernel(GemmParams p, int ngroups) {
     __shared__ uint4 As[2][16 * MAXRB * (U * 8 + 1)];
     const int nt = *p.ntiles;
     const int nitems = nt * ngroups;
-    for (int item = blockIdx.x; item < nitems; item += gridDim.x)
-        stream_item<WF, EPI, U, MAXRB>(p, item % nt, item / nt, As);
+    const int per_xcd = (nitems + 7) / 8;
+    const int local = blockIdx.x / 8;
+    if (local >= per_xcd) return;
+    const int item = (blockIdx.x % 8) * per_xcd + local;
+    if (item >= nitems) return;
+    stream_item<WF, EPI, U, MAXRB, NB>(p, item % nt, item / nt, As);
 }
 
 // ------------------------------------------------------------------ bf16, LDS-tiled form
@@ -1049,17 +1097,14 @@ __global__ __launch_bounds__(256) void reduce_splits_kernel(const float* __restr
     out[i] = s;
 }
 
-// Streaming (decode) form: one (tile, column group) item per work-group.
-template <int EPI, int U>
+// Streaming (decode) form: one (tile, column group) item per work-group; NB 16-column
+// blocks per wavefront.
+template <int EPI, int U, int NB>
 int stream_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, const char* name) {
-    const int ngroups = (EPI == EPI_SWIGLU) ? ceil_div(p.ncols, 32) : ceil_div(p.ncols, 64);
-    const long long items = (long long)ntiles_max * ngroups;
+    const int ngroups = (EPI == EPI_SWIGLU) ? ceil_div(p.ncols, 32 * NB) : ceil_div(p.ncols, 64 * NB);
+    const long long items = 8LL * ceil_div(ntiles_max * ngroups, 8);
     if (items <= 0) return YVMOE_OK;
-#define YV_ST(WFV)                                                                           \
-    do {                                                                                     \
-        /* one item per work-group measured best; the kernel also runs persistent grids */ \
-        gemm_stream_kernel<WFV, EPI, U, 1><<<(unsigned)items, 256, 0, st>>>(p, ngroups);     \
-    } while (0)
+#define YV_ST(WFV) gemm_stream_kernel<WFV, EPI, U, 1, NB><<<(unsigned)items, 256, 0, st>>>(p, ngroups)
     switch (wf) {
         case YVMOE_W_BF16: YV_ST(YVMOE_W_BF16); break;
         case YVMOE_W_INT8: YV_ST(YVMOE_W_INT8); break;
@@ -1237,7 +1282,7 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.kchunk = H;
     const bool streaming = (maxrb == 1);
     int rc = tiled ? tile_dispatch<EPI_SWIGLU>(wf, p, T, st, "expert_gemm1")
-           : streaming ? stream_dispatch<EPI_SWIGLU, 4>(wf, p, T, st, "expert_gemm1")
+           : streaming ? stream_dispatch<EPI_SWIGLU, 4, YV_NB1>(wf, p, T, st, "expert_gemm1")
                        : gemm_dispatch<EPI_SWIGLU>(act, wf, p, T, (F % 32 == 0) ? 2 : 1, 1, st,
                                                    "expert_gemm1", maxrb);
     if (rc != YVMOE_OK) return rc;
@@ -1259,7 +1304,7 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.ldo = H;
     p.kchunk = F;
     if (tiled) return tile_dispatch<EPI_DOWN>(wf, p, T, st, "expert_gemm2");
-    return streaming ? stream_dispatch<EPI_DOWN, 4>(wf, p, T, st, "expert_gemm2")
+    return streaming ? stream_dispatch<EPI_DOWN, 4, YV_NB2>(wf, p, T, st, "expert_gemm2")
                      : gemm_dispatch<EPI_DOWN>(act, wf, p, T, (H % 32 == 0) ? 2 : 1, 1, st,
                                                "expert_gemm2", maxrb);
 }
