@@ -17,7 +17,13 @@ the stream it runs on. Algorithmic bytes per launch = packed weights of the expe
 received tokens + the shared experts + x (N*H*2) + y (rows*H*2); algorithmic FLOPs =
 6*H*F*(N*k + N*S).
 
+roofline.traffic: HBM bytes per launch of the same kernel, from two rocprofv3 counter runs of
+``bench.py --pmc-probe cfg2`` (FETCH_SIZE, then WRITE_SIZE), each scaled by what the counter
+reads for the probe's calibration copy of known size; the measured figures are kept in
+profiles/expert_ffn_cfg2_decode_traffic.json and reported when present.
+
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
+       python bench.py --pmc-probe {cfg2,cfg3}   (launches only, for counter runs)
 """
 import argparse
 import json
@@ -30,6 +36,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "MoE layer tokens/s at 1 GPU; HBM GB/s (decode) & MFMA util % (prefill)"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "expert_ffn_cfg2_decode_traffic.json")
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 
@@ -42,7 +49,42 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prefill-steps", type=int, default=20)
+    ap.add_argument("--pmc-probe", choices=["cfg2", "cfg3"], default=None,
+                    help="run the calibration copy and 5 expert-FFN launches, nothing timed")
     return ap.parse_args()
+
+
+def pmc_probe(name):
+    """Launches for counter collection: a calibration op that reads and writes exactly 256 MiB
+    (int32 bitwise_not), then five yvmoe_expert_ffn launches of the workload."""
+    import torch
+    from pisceslx_amd import functional as yvf
+    from pisceslx_amd.workloads import make_workload, mix_weights, router_state
+    n = 256 * 1024 * 1024 // 4
+    src = torch.arange(n, device="cuda", dtype=torch.int32)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.bitwise_not(src, out=dst)
+    torch.cuda.synchronize()
+    del src, dst
+    w = make_workload(name, device="cuda", seed=0)
+    st = router_state(w)
+    ws = torch.empty(yvf.workspace_bytes(w.n_tokens, 1, st, w.experts), dtype=torch.uint8, device="cuda")
+    routing = yvf.moe_forward(w.x, st, w.experts, mix_weights(w), None, workspace=ws)[2]
+    for _ in range(5):
+        yvf.expert_ffn(w.x, w.experts, routing, w.spec.top_k, workspace=ws)
+    torch.cuda.synchronize()
+    print(f"pmc probe {name}: done", flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per expert-FFN launch at cfg2 from the committed counter summary, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            d = json.load(f)
+        return int(d["hbm_bytes_per_launch"]) if d.get("workload") == "cfg2" else None
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def time_layer(yvf, x, st, experts, mix, skip, ws, steps, warmup):
@@ -94,27 +136,30 @@ def cpu_baseline(w, budget_s=30.0):
     x = w.x.cpu()
     times = []
     t_start = time.perf_counter()
-    moe_oracle.layer_forward(x, params)  # warm-up
+    moe_oracle.layer_forward(x, params, reference_linear=True)  # warm-up
     for _ in range(3):
         if time.perf_counter() - t_start > budget_s and times:
             break
         t0 = time.perf_counter()
-        moe_oracle.layer_forward(x, params)
+        moe_oracle.layer_forward(x, params, reference_linear=True)
         times.append(time.perf_counter() - t0)
     t = statistics.median(times)
     return {"value": round(w.n_tokens / t, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
             "sample": f"{w.spec.name} full forward, {w.n_tokens} tokens, 1 warm-up + median of "
-                      f"{len(times)} runs ({t:.3f} s each), experts dequantized inside the loop"}
+                      f"{len(times)} runs ({t:.3f} s each), experts dequantized inside the loop, "
+                      f"bf16 F.linear as the reference runs it"}
 
 
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU only: this build's path (the Yv MoE layer forward) "
-              "runs on one MI355X; multi-GPU sharding is described in DESIGN.md, not run.",
-              file=sys.stderr)
+        print("bench.py measures one GPU only: the Yv MoE layer forward runs on one MI355X "
+              "here; runs over several GPUs are not part of this benchmark.", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_probe:
+        pmc_probe(args.pmc_probe)
+        return
     import torch
     from pisceslx_amd import functional as yvf
     from pisceslx_amd.workloads import make_workload, mix_weights, router_state, seq_lengths
@@ -151,7 +196,8 @@ def main():
                    "top_k": spec.top_k, "shared_experts": spec.num_shared,
                    "weights": "int8 per-output-channel, bf16 scales", "seed": 0},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(),
                      "kernel": "grouped expert FFN (yvmoe_expert_ffn)",
                      "ms_per_launch": round(t_ffn * 1e3, 4),
                      "algorithmic_bytes": work["bytes"], "active_experts": work["active_experts"]},

@@ -212,22 +212,26 @@ def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     return (x.double() @ w.double().t()).to(x.dtype)
 
 
-def swiglu(xs: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, wd: torch.Tensor) -> torch.Tensor:
+def swiglu(xs: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, wd: torch.Tensor, lin=linear) -> torch.Tensor:
     """YvSwiGLUExpert.forward (expert.py:484-489) in the dtype of its inputs."""
-    return linear(F.silu(linear(xs, wg)) * linear(xs, wu), wd)
+    return lin(F.silu(lin(xs, wg)) * lin(xs, wu), wd)
 
 
 def layer_forward(x2d: torch.Tensor, params: LayerParams, logits: Optional[np.ndarray] = None,
                   cap: Optional[int] = None, skip: Optional[torch.Tensor] = None,
                   routing: Optional[OracleRouting] = None,
-                  tokens: Optional[np.ndarray] = None) -> Dict[str, object]:
+                  tokens: Optional[np.ndarray] = None,
+                  reference_linear: bool = False) -> Dict[str, object]:
     """Reference forward of one packed batch x2d [N, H] (CPU, layer dtype = x2d.dtype).
 
     logits / cap / routing may be supplied to check the GPU path "given identical fp32 gate
     logits". ``tokens`` restricts the expert math to a subset of tokens (rows of other
     tokens are left zero): given the routing, tokens are independent. Returns out [N,H],
-    shared [N,H] (or None) and the routing.
+    shared [N,H] (or None) and the routing. ``reference_linear`` runs the GEMMs as the
+    reference does on the CPU (``F.linear`` in the layer dtype, torch's own accumulation
+    order) instead of correctly rounded: the timed CPU baseline uses it, the checks do not.
     """
+    lin = (lambda a, b: F.linear(a, b)) if reference_linear else linear
     dtype = x2d.dtype
     N, H = x2d.shape
     E, S, k = params.num_experts, params.num_shared, params.top_k
@@ -254,7 +258,7 @@ def layer_forward(x2d: torch.Tensor, params: LayerParams, logits: Optional[np.nd
             continue
         rows = torch.from_numpy(token_of[sel].astype(np.int64))
         wg, wu, wd = params.expert(e)
-        ye = swiglu(x2d[rows], wg.to(dtype), wu.to(dtype), wd.to(dtype))
+        ye = swiglu(x2d[rows], wg.to(dtype), wu.to(dtype), wd.to(dtype), lin)
         Y[torch.from_numpy(sel)] = ye.float()
     # weighted combine (fused_moe.py:117-119): per token, slots j = 0..k-1 in order,
     # multiply then add in fp32 (the reference's GPU index_add_ is atomic and unordered)
@@ -276,8 +280,8 @@ def layer_forward(x2d: torch.Tensor, params: LayerParams, logits: Optional[np.nd
         for s in range(S):
             wg, wu, wd = params.expert(E + s)
             wf = torch.cat([wg, wu], dim=0).to(dtype)  # layer.py:844 fused gate/up
-            g, u = linear(x2d[rows], wf).chunk(2, dim=-1)
-            so = linear(F.silu(g) * u, wd.to(dtype))
+            g, u = lin(x2d[rows], wf).chunk(2, dim=-1)
+            so = lin(F.silu(g) * u, wd.to(dtype))
             shared[rows] = shared[rows] + mix[s].to(dtype) * so
         out = out + shared
         if skip is not None and tuple(skip.shape) == (N, H):
