@@ -24,6 +24,9 @@
  *                           _apply_skip_residual model/moe/layer.py:741-753
  *   yvmoe_forward        -> YvDeepSeekMoELayer.forward / YvDynamicMoELayer.forward
  *                           model/moe/layer.py:1283-1396 / :867-963 (inference)
+ *   yvmoe_moegate_logits -> YvMoEGate.forward in eval mode up to the top-k (steps 2-8 and the
+ *                           loss of step 13), model/moe/gate.py:310-393, :433-444; the top-k
+ *                           and its softmax (gate.py:414-416) are yvmoe_route in fixed mode
  */
 #ifndef YVMOE_H
 #define YVMOE_H
@@ -193,6 +196,72 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
                       const float* mix, const void* skip, void* out, void* shared_out,
                       yvmoe_routing* routing, void* workspace, size_t workspace_bytes,
                       void* stream);
+
+/*
+ * YvMoEGate (model/moe/gate.py:140-451), the router the reference's MoE layers build
+ * (model/moe/layer.py:754-777). Weights as the module holds them, regrouped once:
+ *   w_heads [Rh][H] (activation dtype), Rh = round_up(4E + D, 16): rows [0,E) gate.weight,
+ *           [E,2E) got_cluster_proj.weight, [2E,3E) gate_k.weight, [3E,4E) gate_v.weight,
+ *           [4E,4E+D) input_encoder.0.weight, zero rows after;
+ *   w_dg [dg_dim][H] (activation dtype) hicl_dg_encoder.dg_proj.weight; dg_bias [dg_dim];
+ *   prototypes_t [dg_dim][E] = hicl_prototypesᵀ;
+ *   enc2_t [D][D] = input_encoder.2.weightᵀ;
+ *   expert_enc_t [D][E] = (expert_capability_encoder(expert_embeddings))ᵀ, a constant of
+ *           the weights (gate.py:363);
+ *   modal_affinity [E][n_modalities] expert_modal_affinity; expert_bias [E] or NULL.
+ * All fp32 except w_heads / w_dg. heads: the auxiliary heads computed (YVMOE_HEAD_*; the
+ * reference skips pruned ones, gate.py:263-276). temperature is the effective one of
+ * _safe_temperature (gate.py:297-308), soft_eps = YvNumericalGuard.get_eps(dtype),
+ * capacity_loss = 0.005 · Σ relu(usage - limit)² from the usage buffers (gate.py:586-591).
+ * Limits: H % 64 == 0, dg_dim % 64 == 0 and <= 32768, 1 <= sparsity_k <= min(64, dg_dim),
+ * 1 <= D <= 256.
+ */
+#define YVMOE_HEAD_HICL 1
+#define YVMOE_HEAD_GOT 2
+#define YVMOE_HEAD_SOFT 4
+#define YVMOE_HEAD_EO 8
+
+typedef struct {
+    int32_t num_experts;  /* E */
+    int32_t hidden;       /* H */
+    int32_t enc_dim;      /* D = expert_embed_dim */
+    int32_t dg_dim;       /* hicl_dg_dim = 4H */
+    int32_t sparsity_k;   /* min(32, dg_dim) */
+    int32_t n_modalities;
+    int32_t heads;        /* YVMOE_HEAD_* bits */
+    int32_t reserved;
+    const void* w_heads;
+    const void* w_dg;
+    const float* dg_bias;
+    const float* prototypes_t;
+    const float* enc2_t;
+    const float* expert_enc_t;
+    const float* modal_affinity;
+    const float* expert_bias;
+    float w_hicl, w_got, w_soft, w_eo;
+    float soft_temperature;
+    float temperature;
+    float soft_eps;
+    float load_balance_alpha;
+    float z_loss_alpha;
+    float soft_budget;
+    float capacity_loss;
+    float reserved_f;
+} yvmoe_moegate;
+
+size_t yvmoe_moegate_workspace_bytes(int32_t n_tokens, int32_t act_dtype, const yvmoe_moegate* gate);
+
+/*
+ * logits [N][E] fp32: the temperature-scaled logits the gate's softmax and top-k run on;
+ * loss [1] fp32: load balance + capacity + z-loss + SoftMoE budget terms of the eval
+ * forward (NaN for N = 0, as the reference's means over no tokens). modal_id [N] int32 (one
+ * modality per token) or NULL; ids outside [0, n_modalities) add nothing (the module checks
+ * them before the call). Route with yvmoe_route on (logits, ld = E) and a yvmoe_router with
+ * fixed_shape_mode = 1 and bias = NULL.
+ */
+int32_t yvmoe_moegate_logits(const void* x, int32_t act_dtype, int32_t n_tokens,
+                             const yvmoe_moegate* gate, const int32_t* modal_id, float* logits,
+                             float* loss, void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

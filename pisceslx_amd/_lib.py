@@ -46,7 +46,15 @@ EXPORTED_SYMBOLS = (
     "yvmoe_expert_ffn",
     "yvmoe_combine",
     "yvmoe_forward",
+    "yvmoe_moegate_workspace_bytes",
+    "yvmoe_moegate_logits",
 )
+
+# YvMoEGate auxiliary heads (YVMOE_HEAD_*)
+HEAD_HICL = 1
+HEAD_GOT = 2
+HEAD_SOFT = 4
+HEAD_EO = 8
 
 
 class ExpertWeights(ctypes.Structure):
@@ -94,6 +102,39 @@ class Routing(ctypes.Structure):
     ]
 
 
+class MoEGate(ctypes.Structure):
+    _fields_ = [
+        ("num_experts", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("enc_dim", ctypes.c_int32),
+        ("dg_dim", ctypes.c_int32),
+        ("sparsity_k", ctypes.c_int32),
+        ("n_modalities", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("w_heads", ctypes.c_void_p),
+        ("w_dg", ctypes.c_void_p),
+        ("dg_bias", ctypes.c_void_p),
+        ("prototypes_t", ctypes.c_void_p),
+        ("enc2_t", ctypes.c_void_p),
+        ("expert_enc_t", ctypes.c_void_p),
+        ("modal_affinity", ctypes.c_void_p),
+        ("expert_bias", ctypes.c_void_p),
+        ("w_hicl", ctypes.c_float),
+        ("w_got", ctypes.c_float),
+        ("w_soft", ctypes.c_float),
+        ("w_eo", ctypes.c_float),
+        ("soft_temperature", ctypes.c_float),
+        ("temperature", ctypes.c_float),
+        ("soft_eps", ctypes.c_float),
+        ("load_balance_alpha", ctypes.c_float),
+        ("z_loss_alpha", ctypes.c_float),
+        ("soft_budget", ctypes.c_float),
+        ("capacity_loss", ctypes.c_float),
+        ("reserved_f", ctypes.c_float),
+    ]
+
+
 _LIB: Optional[ctypes.CDLL] = None
 
 
@@ -118,6 +159,10 @@ def _declare(l: ctypes.CDLL) -> None:
     l.yvmoe_combine.restype = i32
     l.yvmoe_combine.argtypes = [vp, i32, i32, i32, i32, i32, ctypes.POINTER(Routing), vp, vp,
                                 vp, vp, vp]
+    l.yvmoe_moegate_workspace_bytes.restype = sz
+    l.yvmoe_moegate_workspace_bytes.argtypes = [i32, i32, ctypes.POINTER(MoEGate)]
+    l.yvmoe_moegate_logits.restype = i32
+    l.yvmoe_moegate_logits.argtypes = [vp, i32, i32, ctypes.POINTER(MoEGate), vp, vp, vp, vp, sz, vp]
     l.yvmoe_forward.restype = i32
     l.yvmoe_forward.argtypes = [vp, i32, i32, ctypes.POINTER(Router), ctypes.POINTER(ExpertWeights),
                                 vp, vp, vp, vp, ctypes.POINTER(Routing), vp, sz, vp]

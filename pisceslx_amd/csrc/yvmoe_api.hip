@@ -255,4 +255,58 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
                           skip, out, shared_out, st);
 }
 
+static int check_moegate(const yvmoe_moegate* g, int act) {
+    YV_REQUIRE(g != nullptr, YVMOE_ERR_ARG, "gate is NULL");
+    YV_REQUIRE(act == YVMOE_ACT_F32 || act == YVMOE_ACT_BF16, YVMOE_ERR_DTYPE,
+               "unknown activation dtype %d", act);
+    YV_REQUIRE(g->num_experts >= 1 && g->num_experts <= YVMOE_MAX_EXPERTS, YVMOE_ERR_SHAPE,
+               "num_experts=%d outside [1, %d]", g->num_experts, YVMOE_MAX_EXPERTS);
+    YV_REQUIRE(g->hidden > 0 && g->hidden % 64 == 0, YVMOE_ERR_SHAPE,
+               "hidden=%d must be a positive multiple of 64", g->hidden);
+    YV_REQUIRE(g->heads >= 0 && g->heads <= 15, YVMOE_ERR_ARG, "heads=%d", g->heads);
+    YV_REQUIRE(g->enc_dim >= 1 && g->enc_dim <= 256, YVMOE_ERR_SHAPE, "enc_dim=%d outside [1, 256]",
+               g->enc_dim);
+    YV_REQUIRE(g->w_heads != nullptr, YVMOE_ERR_ARG, "w_heads is NULL");
+    YV_REQUIRE(g->temperature > 0.f && g->soft_temperature != 0.f, YVMOE_ERR_ARG,
+               "temperature=%g soft_temperature=%g", g->temperature, g->soft_temperature);
+    YV_REQUIRE(g->n_modalities >= 0, YVMOE_ERR_ARG, "n_modalities=%d", g->n_modalities);
+    if (g->heads & YVMOE_HEAD_HICL) {
+        YV_REQUIRE(g->dg_dim > 0 && g->dg_dim % 64 == 0 && g->dg_dim <= 32768, YVMOE_ERR_SHAPE,
+                   "dg_dim=%d must be a positive multiple of 64 up to 32768", g->dg_dim);
+        YV_REQUIRE(g->sparsity_k >= 1 && g->sparsity_k <= 64 && g->sparsity_k <= g->dg_dim,
+                   YVMOE_ERR_SHAPE, "sparsity_k=%d outside [1, min(64, dg_dim)]", g->sparsity_k);
+        YV_REQUIRE(g->w_dg && g->dg_bias && g->prototypes_t, YVMOE_ERR_ARG,
+                   "HiCL head needs w_dg, dg_bias and prototypes_t");
+    }
+    if (g->heads & YVMOE_HEAD_EO)
+        YV_REQUIRE(g->enc2_t && g->expert_enc_t, YVMOE_ERR_ARG,
+                   "expert-oriented head needs enc2_t and expert_enc_t");
+    return YVMOE_OK;
+}
+
+size_t yvmoe_moegate_workspace_bytes(int32_t n_tokens, int32_t act_dtype, const yvmoe_moegate* gate) {
+    if (n_tokens < 0 || check_moegate(gate, act_dtype) != YVMOE_OK) return 0;
+    return gate_ws(n_tokens, act_dtype, gate).bytes;
+}
+
+int32_t yvmoe_moegate_logits(const void* x, int32_t act_dtype, int32_t n_tokens,
+                             const yvmoe_moegate* gate, const int32_t* modal_id, float* logits,
+                             float* loss, void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = check_moegate(gate, act_dtype);
+    if (rc) return rc;
+    YV_REQUIRE(n_tokens >= 0, YVMOE_ERR_ARG, "n_tokens=%d < 0", n_tokens);
+    YV_REQUIRE(loss != nullptr, YVMOE_ERR_ARG, "loss is NULL");
+    YV_REQUIRE(n_tokens == 0 || (x && logits), YVMOE_ERR_ARG, "NULL pointer");
+    YV_REQUIRE(modal_id == nullptr || (gate->modal_affinity && gate->n_modalities > 0),
+               YVMOE_ERR_ARG, "modal_id needs modal_affinity");
+    YV_REQUIRE((long long)n_tokens * (gate->dg_dim > 0 ? gate->dg_dim : 1) < (1ll << 40),
+               YVMOE_ERR_SHAPE, "problem too large");
+    const size_t need = gate_ws(n_tokens, act_dtype, gate).bytes;
+    YV_REQUIRE(workspace != nullptr && workspace_bytes >= need, YVMOE_ERR_WORKSPACE,
+               "workspace %zu bytes, need %zu", workspace_bytes, need);
+    return moegate_launch(x, act_dtype, n_tokens, gate, modal_id, logits, loss, (char*)workspace,
+                          (hipStream_t)stream);
+}
+
 }  // extern "C"

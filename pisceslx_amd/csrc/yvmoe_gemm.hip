@@ -1181,6 +1181,37 @@ int gemm_dispatch(int act, int wf, GemmParams p, int ntiles_max, int ncb, int ks
 
 }  // namespace
 
+int dense_gemm_launch(const void* x, int act, int N, int K, const void* w, int ncols, float* out,
+                      int ld, float* partials, hipStream_t st, const char* name) {
+    if (N <= 0) return YVMOE_OK;
+    GemmParams p{};
+    p.A = x;
+    p.lda = K;
+    p.rowmap = nullptr;
+    p.B0 = w;
+    p.K = K;
+    p.ncols = ncols;
+    p.ldo = ld;
+    p.nrows = N;
+    const int wf = (act == YVMOE_ACT_F32) ? YVMOE_W_F32 : YVMOE_W_BF16;
+    const int ks = dense_ksplit(N, ncols, K);
+    const int ncb = (ncols % 32 == 0) ? 2 : 1;
+    if (ks == 1 || partials == nullptr) {
+        p.kchunk = K;
+        p.out = out;
+        return gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), ncb, 1, st, name);
+    }
+    p.kchunk = K / ks;
+    p.out = partials;
+    p.split_stride = (long long)N * ld;
+    int rc = gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), ncb, ks, st, name);
+    if (rc) return rc;
+    const long long n = (long long)N * ld;
+    reduce_splits_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(partials, ks, n, n, out);
+    YV_LAUNCH_CHECK("dense_gemm_reduce");
+    return YVMOE_OK;
+}
+
 int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, float* out, int ld,
                        float* partials, hipStream_t st, bool reduce) {
     GemmParams p{};

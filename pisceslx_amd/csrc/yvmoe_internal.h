@@ -59,6 +59,14 @@ inline int router_ksplit(int N, int E, int act, int H) {
     return ks;
 }
 
+// K splits of a dense fp32-output GEMM over ncols columns (same rule as the router's).
+inline int dense_ksplit(int N, int ncols, int K) {
+    const int wgs = ceil_div(N > 0 ? N : 1, 64) * ceil_div(ncols, 64);
+    int ks = 1;
+    while (wgs * ks * 2 <= 512 && K % (ks * 2 * 64) == 0 && K / (ks * 2) >= 128) ks *= 2;
+    return ks;
+}
+
 inline size_t router_partials_bytes(int N, int E, int act, int H) {
     const int ks = router_ksplit(N, E, act, H);
     return ks > 1 ? align_up((size_t)ks * N * router_ld(E, act) * 4, 256) : 0;
@@ -146,6 +154,20 @@ TileTable ffn_tile_table(int N, int k, int E, int S, int F, int act, int tile_ro
 int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_weights* w,
                       const yvmoe_routing* routing, void* y, char* ws, hipStream_t st,
                       bool tiles_ready = false);
+// out[N][ld] (fp32) = x[N][K] · wᵀ, w [ncols][K] in the activation dtype; split-K partial
+// sums (when the rule splits) go to partials and are reduced in split order.
+int dense_gemm_launch(const void* x, int act, int N, int K, const void* w, int ncols, float* out,
+                      int ld, float* partials, hipStream_t st, const char* name);
+// YvMoEGate logits and loss (yvmoe_moegate.hip). Workspace: heads GEMM output [N][Rh],
+// DG activations [N][dg_dim], split-K partial sums of either GEMM, per-work-group loss sums.
+struct GateWs {
+    size_t heads, dg, partials, loss, bytes;
+    int groups;
+};
+int moegate_heads_rows(const yvmoe_moegate* g);
+GateWs gate_ws(int N, int act, const yvmoe_moegate* g);
+int moegate_launch(const void* x, int act, int N, const yvmoe_moegate* g, const int* modal_id,
+                   float* logits, float* loss, char* ws, hipStream_t st);
 int combine_launch(const void* y, int act, int N, int H, int k, int S,
                    const yvmoe_routing* routing, const float* mix, const void* skip,
                    void* out, void* shared_out, hipStream_t st);

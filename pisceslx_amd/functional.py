@@ -196,3 +196,83 @@ def moe_forward(x2d: torch.Tensor, router: RouterState, experts: PackedExperts,
                                          ctypes.byref(o), workspace.data_ptr(), workspace.numel(),
                                          _stream(dev)), "yvmoe_forward")
     return out, shared_out, routing
+
+
+@dataclass
+class MoEGateState:
+    """Device tensors and constants of one YvMoEGate, regrouped for yvmoe_moegate_logits."""
+
+    num_experts: int
+    hidden: int
+    enc_dim: int
+    dg_dim: int
+    sparsity_k: int
+    n_modalities: int
+    heads: int                      # _lib.HEAD_* bits
+    w_heads: torch.Tensor           # [Rh, H] activation dtype
+    w_dg: Optional[torch.Tensor]    # [dg, H] activation dtype
+    dg_bias: Optional[torch.Tensor]
+    prototypes_t: Optional[torch.Tensor]
+    enc2_t: Optional[torch.Tensor]
+    expert_enc_t: Optional[torch.Tensor]
+    modal_affinity: Optional[torch.Tensor]
+    expert_bias: Optional[torch.Tensor]
+    w_hicl: float
+    w_got: float
+    w_soft: float
+    w_eo: float
+    soft_temperature: float
+    temperature: float
+    soft_eps: float
+    load_balance_alpha: float
+    z_loss_alpha: float
+    soft_budget: float
+    capacity_loss: float
+
+    def tensors(self):
+        return [t for t in (self.w_heads, self.w_dg, self.dg_bias, self.prototypes_t, self.enc2_t,
+                            self.expert_enc_t, self.modal_affinity, self.expert_bias)
+                if t is not None]
+
+    def struct(self) -> _lib.MoEGate:
+        return _lib.MoEGate(
+            self.num_experts, self.hidden, self.enc_dim, self.dg_dim, self.sparsity_k,
+            self.n_modalities, self.heads, 0, _ptr(self.w_heads), _ptr(self.w_dg),
+            _ptr(self.dg_bias), _ptr(self.prototypes_t), _ptr(self.enc2_t),
+            _ptr(self.expert_enc_t), _ptr(self.modal_affinity), _ptr(self.expert_bias),
+            self.w_hicl, self.w_got, self.w_soft, self.w_eo, self.soft_temperature,
+            self.temperature, self.soft_eps, self.load_balance_alpha, self.z_loss_alpha,
+            self.soft_budget, self.capacity_loss, 0.0)
+
+
+def moegate_workspace_bytes(n_tokens: int, act: int, gate: MoEGateState) -> int:
+    g = gate.struct()
+    return int(_lib.lib().yvmoe_moegate_workspace_bytes(n_tokens, act, ctypes.byref(g)))
+
+
+def moegate_logits(x2d: torch.Tensor, gate: MoEGateState, modal_id: Optional[torch.Tensor] = None,
+                   workspace: Optional[torch.Tensor] = None):
+    """YvMoEGate logits [N, E] fp32 (temperature-scaled) and the routing loss [1] fp32."""
+    dev = _require_cuda(x2d, modal_id, *gate.tensors())
+    act = _act(x2d.dtype)
+    N, H = x2d.shape
+    if H != gate.hidden:
+        raise ValueError(f"hidden size {H} does not match the gate ({gate.hidden})")
+    if modal_id is not None and (modal_id.dtype != torch.int32 or modal_id.numel() != N):
+        raise ValueError("modal_id must be int32 [N]")
+    E = gate.num_experts
+    logits = torch.empty(N, E, dtype=torch.float32, device=dev)
+    loss = torch.empty(1, dtype=torch.float32, device=dev)
+    need = moegate_workspace_bytes(N, act, gate)
+    if need == 0:
+        raise ValueError("yvmoe_moegate_workspace_bytes rejected the gate state")
+    if workspace is None or workspace.numel() < need:
+        workspace = _workspace(need, dev)
+    g = gate.struct()
+    _lib.check(_lib.lib().yvmoe_moegate_logits(x2d.data_ptr() if N > 0 else None, act, N,
+                                                ctypes.byref(g), _ptr(modal_id),
+                                                logits.data_ptr() if N > 0 else None,
+                                                loss.data_ptr(), workspace.data_ptr(),
+                                                workspace.numel(), _stream(dev)),
+               "yvmoe_moegate_logits")
+    return logits, loss

@@ -23,6 +23,7 @@ from typing import Optional
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from . import _lib
 from . import functional as yvf
@@ -150,3 +151,248 @@ class YvStableMoEGate(nn.Module):
         st = self.router_state(_lib.ACT_F32)
         cap = -1 if capacity is None else int(capacity)
         return yvf.route(logits.float().contiguous(), st, predictor=False, capacity_override=cap)
+
+
+class _YvDGEncoder(nn.Module):
+    """Parameters of YvDGEncoder (model/moe/hicl_router.py:50-85): dg_proj and dg_bias; the
+    relu / top-k / L2 normalisation run in the gate kernel."""
+
+    def __init__(self, hidden_size, expansion_factor=4, sparsity_k=32, device=None, dtype=None):
+        super().__init__()
+        self.hidden_size = hidden_size
+        self.dg_dim = hidden_size * expansion_factor
+        self.sparsity_k = sparsity_k
+        self.dg_proj = nn.Linear(hidden_size, self.dg_dim, bias=False, device=device, dtype=dtype)
+        self.register_buffer("dg_bias", torch.zeros(self.dg_dim, device=device, dtype=dtype))
+
+
+class YvMoEGate(nn.Module):
+    """YvMoEGate for MI355X: the router the reference's MoE layers build (layer.py:754-777).
+
+    Mirrors ``YvMoEGate`` (model/moe/gate.py:140-451): same constructor arguments, parameter
+    and buffer names, ``forward(x, modal_id=None) -> (top_scores, top_idx, loss)``. Inference
+    only: the standard gate plus the four auxiliary heads (HiCL, Graph-of-Tokens cluster
+    projection, SoftMoE, Expert-Oriented), modal affinity, expert bias and temperature run in
+    ``yvmoe_moegate_logits``; the softmax / top-k / softmax of the k scores in ``yvmoe_route``
+    (fixed mode); the PathMoE stage cache (gate.py:418-431) is kept on the module.
+
+    Differences a caller can observe, all deliberate:
+    * logits are computed in fp32 whatever the parameter dtype (the reference's chain runs in
+      the parameter dtype); ``top_scores`` are the fp32 softmax cast to x's dtype, as the
+      reference casts them (gate.py:416);
+    * ``got_graph_builder`` (whose output the reference computes under no_grad and never
+      uses, gate.py:345-346) and ``importance_proj`` (whose tiers the top-k never reads,
+      gate.py:396-402) are not built; their keys in a reference state_dict are skipped on load;
+    * training-mode forwards raise NotImplementedError;
+    * after ``prune_routing_heads`` the pruned heads are left out of the logits, as
+      ``_should_compute_aux_head`` intends (gate.py:263-276); the reference's forward instead
+      raises AttributeError, since it reads the deleted ``sparse_gate_*`` before that check
+      (gate.py:331-333).
+    """
+
+    HEAD_NAMES = (("hicl", _lib.HEAD_HICL), ("got", _lib.HEAD_GOT),
+                  ("soft_moe", _lib.HEAD_SOFT), ("expert_orient", _lib.HEAD_EO))
+    _SKIPPED_PREFIXES = ("got_graph_builder.", "importance_proj.")
+
+    def __init__(self, hidden_size, num_experts, top_k=2, device=None, dtype=None,
+                 load_balance_alpha=0.01, noise_std=0.1, enable_cognitive_density=False,
+                 expert_capacity_limit=1.2, dynamic_top_k_min=1, dynamic_top_k_max=3,
+                 load_balance_threshold=0.15, cfg=None):
+        super().__init__()
+        if not 1 <= num_experts <= _lib.MAX_EXPERTS:
+            raise ValueError(f"num_experts={num_experts} outside [1, {_lib.MAX_EXPERTS}]")
+        c = lambda name, default: getattr(cfg, name, default) if cfg is not None else default
+        f = dict(device=device, dtype=dtype)
+        self.top_k = top_k
+        self.num_experts = num_experts
+        self.hidden_size = hidden_size
+        self.load_balance_alpha = load_balance_alpha
+        self.noise_std = max(noise_std, 0.2)
+        self.enable_cognitive_density = enable_cognitive_density
+        self.expert_capacity_limit = expert_capacity_limit
+        self.dynamic_top_k_min = dynamic_top_k_min
+        self.dynamic_top_k_max = dynamic_top_k_max
+        self.load_balance_threshold = load_balance_threshold
+        self.z_loss_alpha = c("moe_z_loss_alpha", 1e-4)
+        self.random_to_gradient_steps = c("moe_random_to_gradient_steps", 2000)
+        self.attention_mamba_temp = c("moe_attention_mamba_temp", 0.3)
+        self.min_temperature = c("moe_temperature_min", 1.5)
+        self.register_buffer("expert_usage_count", torch.zeros(num_experts, **f))
+        self.register_buffer("temperature", torch.tensor(c("moe_routing_temperature", 3.0), **f))
+        self.register_buffer("total_routing_count", torch.tensor(0.0, **f))
+        self.register_buffer("expert_temperature_max", torch.tensor(c("moe_temperature_max", 5.0), **f))
+        self.register_buffer("expert_bias", torch.zeros(num_experts, **f))
+        self.register_buffer("bias_update_counter", torch.tensor(0, **f))
+        self._is_checkpointing = False
+        self.gate = nn.Linear(hidden_size, num_experts, bias=False, **f)
+        # HiCL
+        self.hicl_dg_dim = hidden_size * 4
+        self.hicl_dg_encoder = _YvDGEncoder(hidden_size, 4, 32, **f)
+        self.hicl_prototypes = nn.Parameter(torch.randn(num_experts, self.hicl_dg_dim, **f) * 0.02)
+        self.w_hicl = nn.Parameter(torch.tensor(0.1, **f))
+        # Graph-of-Tokens: only the cluster projection reaches the logits
+        self.got_cluster_proj = nn.Linear(hidden_size, num_experts, bias=False, **f)
+        self.w_got = nn.Parameter(torch.tensor(0.05, **f))
+        # SoftMoE
+        self.soft_moe_temperature = c("soft_moe_temperature", 1.0)
+        self.gate_k = nn.Linear(hidden_size, num_experts, bias=False, **f)
+        self.gate_v = nn.Linear(hidden_size, num_experts, bias=False, **f)
+        self.register_buffer("soft_moe_budget", torch.tensor(float(c("soft_moe_mean_k", top_k)), **f))
+        self.w_soft = nn.Parameter(torch.tensor(0.05, **f))
+        # Expert-Oriented
+        D = max(64, hidden_size // 64)
+        self.expert_embeddings = nn.Parameter(torch.randn(num_experts, D, **f))
+        self.input_encoder = nn.Sequential(nn.Linear(hidden_size, D, bias=False, **f), nn.SiLU(),
+                                           nn.Linear(D, D, bias=False, **f))
+        self.expert_capability_encoder = nn.Sequential(nn.Linear(D, D, bias=False, **f), nn.SiLU(),
+                                                       nn.Linear(D, D, bias=False, **f))
+        self.w_expert_orient = nn.Parameter(torch.tensor(0.05, **f))
+        # Modal-aware affinity (n_modalities 7 without a cfg, as gate.py:247)
+        self.n_modalities = c("n_modalities", 5) if cfg is not None else 7
+        self.expert_modal_affinity = nn.Parameter(torch.zeros(num_experts, self.n_modalities, **f))
+        self.affinity_alpha = 1.0
+        # PathMoE cache
+        self._path_moe_stage_size = c("path_moe_stage_size", 4)
+        self._path_moe_layer_idx = 0
+        self._path_moe_cache = None
+        self._path_moe_signature = None
+        self.sparse_gate_hicl = nn.Parameter(torch.tensor(5.0, **f))
+        self.sparse_gate_got = nn.Parameter(torch.tensor(5.0, **f))
+        self.sparse_gate_soft_moe = nn.Parameter(torch.tensor(5.0, **f))
+        self.sparse_gate_expert_orient = nn.Parameter(torch.tensor(5.0, **f))
+        self._pruned_heads: set = set()
+        self._state = None
+        self._state_key = None
+        self._register_load_state_dict_pre_hook(self._skip_unbuilt_keys)
+        self.last_routing: Optional[yvf.Routing] = None
+
+    def _skip_unbuilt_keys(self, state_dict, prefix, *args):
+        for k in [k for k in state_dict if k.startswith(tuple(prefix + p for p in self._SKIPPED_PREFIXES))]:
+            del state_dict[k]
+
+    # ------------------------------------------------------------ host-side state
+    def _host_constants(self, seq_len: int):
+        """Effective temperature (gate.py:297-308) and the capacity term (gate.py:586-591),
+        both from buffers, evaluated in the buffers' dtype as the reference does."""
+        t = self.temperature.detach().cpu()
+        if seq_len >= 8192:
+            t = t * self.attention_mamba_temp
+        hi = self.expert_temperature_max.detach().cpu().to(t.dtype)
+        t = torch.max(torch.min(t, hi), torch.tensor(0.1, dtype=t.dtype))
+        cap = 0.0
+        total = self.total_routing_count.detach().cpu()
+        if float(total) > 0:
+            usage = self.expert_usage_count.detach().cpu() / total
+            cap = float(0.005 * torch.sum(torch.relu(usage - self.expert_capacity_limit) ** 2))
+        return float(t), cap
+
+    def gate_state(self, act: int, seq_len: int) -> yvf.MoEGateState:
+        """Regrouped device tensors for yvmoe_moegate_logits (rebuilt when a parameter,
+        buffer or the pruned set changes)."""
+        tensors = list(self.parameters()) + list(self.buffers())
+        key = (act, seq_len >= 8192, tuple(sorted(self._pruned_heads)),
+               tuple((t.data_ptr(), t._version) for t in tensors))
+        if self._state is not None and self._state_key == key:
+            return self._state
+        wdt = torch.bfloat16 if act == _lib.ACT_BF16 else torch.float32
+        E, H = self.num_experts, self.hidden_size
+        D = self.expert_embeddings.shape[1]
+        heads = 0
+        for name, bit in self.HEAD_NAMES:
+            if name not in self._pruned_heads:
+                heads |= bit
+        with torch.no_grad():
+            dev = self.gate.weight.device
+            rh = (4 * E + D + 15) // 16 * 16
+            w_heads = torch.zeros(rh, H, dtype=wdt, device=dev)
+            w_heads[0:E] = self.gate.weight
+            w_heads[E:2 * E] = self.got_cluster_proj.weight
+            w_heads[2 * E:3 * E] = self.gate_k.weight
+            w_heads[3 * E:4 * E] = self.gate_v.weight
+            w_heads[4 * E:4 * E + D] = self.input_encoder[0].weight
+            enc = self.hicl_dg_encoder
+            w_dg = enc.dg_proj.weight.detach().to(wdt).contiguous()
+            dg_bias = enc.dg_bias.detach().float().contiguous()
+            proto_t = self.hicl_prototypes.detach().float().t().contiguous()
+            enc2_t = self.input_encoder[2].weight.detach().float().t().contiguous()
+            cap0 = self.expert_capability_encoder[0].weight.detach().double()
+            cap2 = self.expert_capability_encoder[2].weight.detach().double()
+            ee = F.silu(self.expert_embeddings.detach().double() @ cap0.t()) @ cap2.t()
+            eenc_t = ee.t().float().contiguous()
+            modal = self.expert_modal_affinity.detach().float().contiguous()
+            ebias = self.expert_bias.detach().float().contiguous()
+        temp, cap_loss = self._host_constants(seq_len)
+        pdt = self.gate.weight.dtype
+        soft_eps = max(1e-8, torch.finfo(pdt).eps * 10) if pdt in (torch.float16, torch.bfloat16) else 1e-8
+        scalar = lambda name: (float(getattr(self, name).detach().float().cpu())
+                               if hasattr(self, name) else 0.0)
+        self._state = yvf.MoEGateState(
+            E, H, D, enc.dg_dim, min(enc.sparsity_k, enc.dg_dim), self.n_modalities, heads,
+            w_heads, w_dg, dg_bias, proto_t, enc2_t, eenc_t, modal, ebias,
+            scalar("w_hicl"), scalar("w_got"), scalar("w_soft"),
+            scalar("w_expert_orient"), float(self.soft_moe_temperature), temp, soft_eps,
+            float(self.load_balance_alpha), float(self.z_loss_alpha),
+            scalar("soft_moe_budget"), cap_loss)
+        self._state_key = key
+        return self._state
+
+    def fixed_router_state(self) -> yvf.RouterState:
+        """The fixed-mode routing (softmax, top-k, softmax of the k scores) on the gate logits."""
+        return yvf.RouterState(self.num_experts, self.hidden_size, min(self.top_k, self.num_experts),
+                               True, False, 0, 1.0, None, None, None, None, None)
+
+    def _modal_ids(self, modal_id: torch.Tensor, B: int, S: int, device) -> torch.Tensor:
+        """modal_id reshaped as gate.py:369-374 does, to int32 [B*S], range-checked."""
+        m = modal_id
+        if tuple(m.shape) != (B, S):
+            m = m.reshape(B, 1).expand(B, S) if m.numel() == B else m.reshape(B, S)
+        m = m.reshape(-1).to(device=device, dtype=torch.int32).contiguous()
+        if m.numel() and (int(m.min()) < -self.n_modalities or int(m.max()) >= self.n_modalities):
+            raise IndexError(f"modal_id outside [-{self.n_modalities}, {self.n_modalities})")
+        return torch.where(m < 0, m + self.n_modalities, m)
+
+    # ------------------------------------------------------------ forward
+    def forward(self, x: torch.Tensor, modal_id: Optional[torch.Tensor] = None):
+        if self.training:
+            raise NotImplementedError("the MI355X YvMoEGate is an inference forward; call .eval() first")
+        B, S, H = x.shape
+        x2d = x.reshape(-1, H).contiguous()
+        act = yvf._act(x2d.dtype)
+        st = self.gate_state(act, S)
+        mid = None if modal_id is None else self._modal_ids(modal_id, B, S, x.device)
+        logits, loss = yvf.moegate_logits(x2d, st, mid)
+        N = x2d.shape[0]
+        # PathMoE (gate.py:418-431): one routing shared by a stage of calls with the same token
+        # count; later calls of a stage keep it (their own logits still set the loss)
+        reuse = False
+        if self._path_moe_stage_size > 1:
+            sig = (N, self.training)
+            if sig != self._path_moe_signature:
+                self._path_moe_layer_idx = 0
+                self._path_moe_cache = None
+                self._path_moe_signature = sig
+            reuse = self._path_moe_layer_idx != 0 and self._path_moe_cache is not None
+        if reuse:
+            routing = self._path_moe_cache
+        else:
+            routing = yvf.route(logits, self.fixed_router_state(), predictor=False)
+            if self._path_moe_stage_size > 1:
+                self._path_moe_cache = routing
+        if self._path_moe_stage_size > 1:
+            self._path_moe_layer_idx = (self._path_moe_layer_idx + 1) % self._path_moe_stage_size
+        self.last_routing = routing
+        self.last_logits = logits
+        self._last_loss_f32 = loss
+        return routing.weights.to(x.dtype), routing.indices, loss.reshape(()).to(x.dtype)
+
+    def prune_routing_heads(self, prune_threshold: float = 0.05) -> None:
+        """Drop auxiliary heads whose sparse gate sigmoid is below the threshold (gate.py:466-489)."""
+        for name, attr in (("hicl", "sparse_gate_hicl"), ("got", "sparse_gate_got"),
+                           ("soft_moe", "sparse_gate_soft_moe"),
+                           ("expert_orient", "sparse_gate_expert_orient")):
+            p = getattr(self, attr, None)
+            if p is not None and float(torch.sigmoid(p.detach().float())) < prune_threshold:
+                self._pruned_heads.add(name)
+                delattr(self, attr)
+                if hasattr(self, f"w_{name}"):
+                    delattr(self, f"w_{name}")

@@ -1,0 +1,158 @@
+"""YvMoEGate on the GPU against the CPU oracle (oracle/moegate_oracle.py).
+
+For each case the module's fp32 logits (yvmoe_moegate_logits) are compared with the oracle's
+float64 logits (max-abs <= 1e-4 · max(1, max |logit|)), the routing is checked bit for bit
+against the C routing oracle given the GPU's logits (indices, weights, counts, permutation),
+``top_scores`` are those weights in x's dtype, and the loss is within 1e-4 relative of the
+oracle's. Cases: the decode shape of the 7B-style layer (hidden 4096, 64 experts, top-6,
+64 tokens), a prefill sample, heads weighted up so every head moves the logits by O(1), exact
+ties at the 32nd DG activation, fewer than 32 positive DG activations, modal ids, a pruned
+head, the long-sequence temperature, fp32 activations, N = 0, determinism, and the PathMoE
+stage cache.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moegate_oracle as mg
+from pisceslx_amd.gate import YvMoEGate
+
+pytestmark = pytest.mark.gpu
+
+
+def _gate(H, E, k, dtype=torch.bfloat16, seed=0, scale_heads=False, stage=1):
+    torch.manual_seed(seed)
+    g = YvMoEGate(H, E, top_k=k, dtype=dtype)
+    with torch.no_grad():
+        g.expert_modal_affinity.normal_(0.0, 0.3)
+        g.expert_bias.normal_(0.0, 0.2)
+        g.hicl_dg_encoder.dg_bias.normal_(0.0, 0.05)
+        if scale_heads:
+            for name in ("w_hicl", "w_got", "w_soft", "w_expert_orient"):
+                getattr(g, name).fill_(1.0)
+            g.hicl_prototypes.mul_(50.0)
+    g._path_moe_stage_size = stage
+    return g.cuda().eval()
+
+
+def _check(g, x, oracle, modal_id=None, heads=None):
+    B, S, H = x.shape
+    E, k = g.num_experts, min(g.top_k, g.num_experts)
+    print(f"moegate B={B} S={S} H={H} E={E} k={k} dtype={x.dtype}", flush=True)
+    scores, idx, loss = g(x, modal_id=modal_id)
+    torch.cuda.synchronize()
+    lg = g.last_logits.cpu().numpy()
+    p = mg.params_from_state_dict(g.state_dict(), g.gate.weight.dtype,
+                                  soft_temperature=g.soft_moe_temperature, heads=heads)
+    o = mg.moegate_forward(x.cpu(), p, k, modal_id=None if modal_id is None else modal_id.cpu())
+    ref = o["logits"].numpy()
+    tol = 1e-4 * max(1.0, float(np.abs(ref).max())) if ref.size else 1e-4
+    err = float(np.abs(lg - ref).max()) if ref.size else 0.0
+    print(f"  logits max_abs={err:.3e} (tol {tol:.1e})", flush=True)
+    assert err <= tol
+    r = oracle.route(lg.astype(np.float32), k, -1, None)
+    routing = g.last_routing
+    assert np.array_equal(idx.cpu().numpy(), r.indices.astype(np.int64))
+    assert np.array_equal(routing.weights.cpu().numpy().view(np.uint32), r.weights.view(np.uint32))
+    assert np.array_equal(routing.counts.cpu().numpy(), r.counts)
+    assert np.array_equal(routing.perm.cpu().numpy(), r.perm)
+    assert scores.dtype == x.dtype and torch.equal(scores, routing.weights.to(x.dtype))
+    got_loss, want_loss = float(loss), o["loss"]
+    print(f"  loss {got_loss:.6e} oracle {want_loss:.6e}", flush=True)
+    if x.dtype == torch.bfloat16:
+        assert got_loss == pytest.approx(float(torch.tensor(want_loss).to(torch.bfloat16)), rel=1e-2)
+    assert float(g._last_loss_f32) == pytest.approx(want_loss, rel=1e-4, abs=1e-7)
+    return o
+
+
+@pytest.mark.parametrize("B,S,H,E,k,scale", [
+    (64, 1, 4096, 64, 6, False),   # 7B-style decode: 64 sequences x 1 token
+    (64, 1, 4096, 64, 6, True),    # every head weighted 1
+    (2, 200, 1024, 8, 2, True),    # small layer, prefill-like
+    (3, 37, 5120, 128, 8, False),  # hidden 5120: DG width 20480
+    (1, 40, 7168, 256, 8, True),   # hidden 7168, 256 experts: DG width 28672
+])
+def test_moegate_matches_oracle(cuda, oracle, B, S, H, E, k, scale):
+    g = _gate(H, E, k, scale_heads=scale, seed=H + E)
+    x = torch.randn(B, S, H, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).cuda()
+    _check(g, x, oracle)
+
+
+def test_dg_ties_and_few_positives(cuda, oracle):
+    H, E = 256, 8
+    g = _gate(H, E, 2, scale_heads=True, seed=1)
+    dg = g.hicl_dg_encoder
+    with torch.no_grad():
+        dg.dg_proj.weight.zero_()           # DG activations = relu(dg_bias) for every token
+        b = torch.full((dg.dg_dim,), -1.0)
+        b[torch.arange(3, 93, 3)] = 2.0     # 30 entries above the threshold
+        b[[700, 5, 1000, 11, 400]] = 1.0     # five-way tie for the last two places
+        dg.dg_bias.copy_(b)
+    x = torch.randn(2, 9, H, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16).cuda()
+    _check(g, x, oracle)
+    with torch.no_grad():                   # 10 positive activations only
+        b = torch.full((dg.dg_dim,), -1.0)
+        b[torch.arange(0, 1000, 100)] = torch.linspace(0.5, 1.5, 10)
+        dg.dg_bias.copy_(b)
+    _check(g, x, oracle)
+    with torch.no_grad():                   # none positive: HiCL adds 0
+        dg.dg_bias.fill_(-1.0)
+    _check(g, x, oracle)
+
+
+def test_modal_ids_and_pruned_head(cuda, oracle):
+    H, E = 512, 16
+    g = _gate(H, E, 4, scale_heads=True, seed=4)
+    x = torch.randn(4, 16, H, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).cuda()
+    _check(g, x, oracle, modal_id=torch.tensor([0, 6, 3, 1]))                    # per sequence
+    _check(g, x, oracle, modal_id=torch.randint(0, 7, (4, 16), generator=torch.Generator().manual_seed(0)))
+    with pytest.raises(IndexError):
+        g(x, modal_id=torch.tensor([0, 7, 3, 1]))
+    with torch.no_grad():
+        g.sparse_gate_got.fill_(-10.0)
+    g.prune_routing_heads(0.05)
+    assert g._pruned_heads == {"got"} and not hasattr(g, "w_got")
+    _check(g, x, oracle, heads=("hicl", "soft_moe", "expert_orient"))
+
+
+def test_long_sequence_temperature_and_fp32(cuda, oracle):
+    H, E = 256, 8
+    g = _gate(H, E, 2, seed=6)
+    x = torch.randn(1, 8192, H, generator=torch.Generator().manual_seed(4)).to(torch.bfloat16).cuda()
+    o = _check(g, x, oracle)
+    assert o["temperature"] == 0.8984375    # bf16(3.0 * 0.3)
+    g32 = _gate(H, E, 2, dtype=torch.float32, seed=7, scale_heads=True)
+    x32 = torch.randn(3, 50, H, generator=torch.Generator().manual_seed(8)).cuda()
+    _check(g32, x32, oracle)
+
+
+def test_empty_batch_and_determinism(cuda, oracle):
+    H, E = 1024, 8
+    g = _gate(H, E, 2, seed=9)
+    s, i, loss = g(torch.zeros(1, 0, H, dtype=torch.bfloat16, device="cuda"))
+    torch.cuda.synchronize()
+    assert s.shape == (0, 2) and i.shape == (0, 2) and torch.isnan(loss)
+    x = torch.randn(8, 300, H, generator=torch.Generator().manual_seed(1)).to(torch.bfloat16).cuda()
+    g(x)
+    a = g.last_logits.clone()
+    la = g._last_loss_f32.clone()
+    g(x)
+    assert torch.equal(a, g.last_logits) and torch.equal(la, g._last_loss_f32)
+
+
+def test_path_moe_stage_cache(cuda):
+    H, E = 256, 8
+    g = _gate(H, E, 2, seed=2, stage=4)
+    gen = torch.Generator().manual_seed(0)
+    xs = [torch.randn(2, 5, H, generator=gen).to(torch.bfloat16).cuda() for _ in range(6)]
+    outs = [g(x)[1].clone() for x in xs[:5]]
+    fresh = [g.last_routing]
+    # calls 2-4 of a stage reuse call 1's routing; call 5 starts a new stage
+    for j in (1, 2, 3):
+        assert torch.equal(outs[j], outs[0])
+    g2 = _gate(H, E, 2, seed=2, stage=1)
+    assert torch.equal(outs[4], g2(xs[4])[1])
+    # another token count resets the stage
+    y = torch.randn(1, 7, H, generator=gen).to(torch.bfloat16).cuda()
+    assert torch.equal(g(y)[1], g2(y)[1])
+    assert fresh[0] is not None
