@@ -200,20 +200,22 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
 /*
  * YvMoEGate (model/moe/gate.py:140-451), the router the reference's MoE layers build
  * (model/moe/layer.py:754-777). Weights as the module holds them, regrouped once:
- *   w_heads [Rh][H] (activation dtype), Rh = round_up(4E + D, 16): rows [0,E) gate.weight,
- *           [E,2E) got_cluster_proj.weight, [2E,3E) gate_k.weight, [3E,4E) gate_v.weight,
- *           [4E,4E+D) input_encoder.0.weight, zero rows after;
- *   w_dg [dg_dim][H] (activation dtype) hicl_dg_encoder.dg_proj.weight; dg_bias [dg_dim];
+ *   w_proj [P][H] (activation dtype), the projections of x in one matrix: with the HiCL head,
+ *           rows [0, dg_dim) hicl_dg_encoder.dg_proj.weight; then Rh = round_up(4E + D, 256)
+ *           head rows: gate.weight, got_cluster_proj.weight, gate_k.weight, gate_v.weight
+ *           (E rows each), input_encoder.0.weight (D rows), zero rows.
+ *           P = dg_dim + Rh with the HiCL head, Rh without;
+ *   dg_bias [dg_dim];
  *   prototypes_t [dg_dim][E] = hicl_prototypesᵀ;
- *   enc2_t [D][D] = input_encoder.2.weightᵀ;
- *   expert_enc_t [D][E] = (expert_capability_encoder(expert_embeddings))ᵀ, a constant of
- *           the weights (gate.py:363);
+ *   eo_mat [D][E] = input_encoder.2.weightᵀ · expert_capability_encoder(expert_embeddings)ᵀ:
+ *           the Expert-Oriented head's two linear maps after the SiLU folded into one constant
+ *           of the weights (gate.py:362-364);
  *   modal_affinity [E][n_modalities] expert_modal_affinity; expert_bias [E] or NULL.
  * All fp32 except w_heads / w_dg. heads: the auxiliary heads computed (YVMOE_HEAD_*; the
  * reference skips pruned ones, gate.py:263-276). temperature is the effective one of
  * _safe_temperature (gate.py:297-308), soft_eps = YvNumericalGuard.get_eps(dtype),
  * capacity_loss = 0.005 · Σ relu(usage - limit)² from the usage buffers (gate.py:586-591).
- * Limits: H % 64 == 0, dg_dim % 64 == 0 and <= 32768, 1 <= sparsity_k <= min(64, dg_dim),
+ * Limits: H % 64 == 0, dg_dim % 256 == 0 and <= 32768, 1 <= sparsity_k <= min(64, dg_dim),
  * 1 <= D <= 256.
  */
 #define YVMOE_HEAD_HICL 1
@@ -230,12 +232,10 @@ typedef struct {
     int32_t n_modalities;
     int32_t heads;        /* YVMOE_HEAD_* bits */
     int32_t reserved;
-    const void* w_heads;
-    const void* w_dg;
+    const void* w_proj;
     const float* dg_bias;
     const float* prototypes_t;
-    const float* enc2_t;
-    const float* expert_enc_t;
+    const float* eo_mat;
     const float* modal_affinity;
     const float* expert_bias;
     float w_hicl, w_got, w_soft, w_eo;

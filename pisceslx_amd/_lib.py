@@ -112,12 +112,10 @@ class MoEGate(ctypes.Structure):
         ("n_modalities", ctypes.c_int32),
         ("heads", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
-        ("w_heads", ctypes.c_void_p),
-        ("w_dg", ctypes.c_void_p),
+        ("w_proj", ctypes.c_void_p),
         ("dg_bias", ctypes.c_void_p),
         ("prototypes_t", ctypes.c_void_p),
-        ("enc2_t", ctypes.c_void_p),
-        ("expert_enc_t", ctypes.c_void_p),
+        ("eo_mat", ctypes.c_void_p),
         ("modal_affinity", ctypes.c_void_p),
         ("expert_bias", ctypes.c_void_p),
         ("w_hicl", ctypes.c_float),

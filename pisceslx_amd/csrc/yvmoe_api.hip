@@ -266,21 +266,20 @@ static int check_moegate(const yvmoe_moegate* g, int act) {
     YV_REQUIRE(g->heads >= 0 && g->heads <= 15, YVMOE_ERR_ARG, "heads=%d", g->heads);
     YV_REQUIRE(g->enc_dim >= 1 && g->enc_dim <= 256, YVMOE_ERR_SHAPE, "enc_dim=%d outside [1, 256]",
                g->enc_dim);
-    YV_REQUIRE(g->w_heads != nullptr, YVMOE_ERR_ARG, "w_heads is NULL");
+    YV_REQUIRE(g->w_proj != nullptr, YVMOE_ERR_ARG, "w_proj is NULL");
     YV_REQUIRE(g->temperature > 0.f && g->soft_temperature != 0.f, YVMOE_ERR_ARG,
                "temperature=%g soft_temperature=%g", g->temperature, g->soft_temperature);
     YV_REQUIRE(g->n_modalities >= 0, YVMOE_ERR_ARG, "n_modalities=%d", g->n_modalities);
     if (g->heads & YVMOE_HEAD_HICL) {
-        YV_REQUIRE(g->dg_dim > 0 && g->dg_dim % 64 == 0 && g->dg_dim <= 32768, YVMOE_ERR_SHAPE,
-                   "dg_dim=%d must be a positive multiple of 64 up to 32768", g->dg_dim);
+        YV_REQUIRE(g->dg_dim > 0 && g->dg_dim % 256 == 0 && g->dg_dim <= 32768, YVMOE_ERR_SHAPE,
+                   "dg_dim=%d must be a positive multiple of 256 up to 32768", g->dg_dim);
         YV_REQUIRE(g->sparsity_k >= 1 && g->sparsity_k <= 64 && g->sparsity_k <= g->dg_dim,
                    YVMOE_ERR_SHAPE, "sparsity_k=%d outside [1, min(64, dg_dim)]", g->sparsity_k);
-        YV_REQUIRE(g->w_dg && g->dg_bias && g->prototypes_t, YVMOE_ERR_ARG,
-                   "HiCL head needs w_dg, dg_bias and prototypes_t");
+        YV_REQUIRE(g->dg_bias && g->prototypes_t, YVMOE_ERR_ARG,
+                   "HiCL head needs dg_bias and prototypes_t");
     }
     if (g->heads & YVMOE_HEAD_EO)
-        YV_REQUIRE(g->enc2_t && g->expert_enc_t, YVMOE_ERR_ARG,
-                   "expert-oriented head needs enc2_t and expert_enc_t");
+        YV_REQUIRE(g->eo_mat != nullptr, YVMOE_ERR_ARG, "expert-oriented head needs eo_mat");
     return YVMOE_OK;
 }
 

@@ -401,7 +401,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
 // column blocks per wavefront put more weight bytes in flight per activation chunk and per
 // barrier.
 template <int WF, int EPI, int U, int MAXRB, int NB>
-__device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int cgroup,
+__device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int cgroup, int kz,
                                             uint4 (&As)[2][16 * MAXRB * (U * 8 + 1)]) {
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
     constexpr bool GROUPED = (WF == YVMOE_W_INT4 || WF == YVMOE_W_FP8);
@@ -415,16 +415,21 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int e = p.tile_seg[tile];
-    const int row0 = p.tile_row0[tile];
-    const int seg_end = p.seg_start[e + 1];
+    // grouped: tiles from the tile table; dense (no table): ROWS-row tiles of nrows rows
+    const bool dense = p.tile_seg == nullptr;
+    const int e = dense ? 0 : p.tile_seg[tile];
+    const int row0 = dense ? tile * ROWS : p.tile_row0[tile];
+    const int seg_end = dense ? p.nrows : p.seg_start[e + 1];
     const int nvalid = min(ROWS, seg_end - row0);
     const int nrb = (nvalid + 15) / 16;
     const int mat = SWIGLU ? (wave & 1) : 0;  // 0: gate (or down), 1: up
     // first column of block b of this wavefront
     const int colw = SWIGLU ? (cgroup * 2 + (wave >> 1)) * 16 * NB : (cgroup * 4 + wave) * 16 * NB;
     const int kl = (lane >> 4) * 16;
-    const int nks = p.K / 64;
+    // K range of split kz (EPI_F32 writes split kz's partial sums at kz * split_stride)
+    const int kbeg = kz * p.kchunk;
+    const int kend = min(p.K, kbeg + p.kchunk);
+    const int nks = (kend - kbeg) / 64;
     const int nchunks = (nks + U - 1) / U;
 
     // staging: thread t copies uint4 q = t + j*256 of each chunk: row q / (U*8), column q % (U*8)
@@ -443,8 +448,8 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
     auto stage_load = [&](int c, uint4 (&v)[PER_THREAD]) {
 #pragma unroll
         for (int j = 0; j < PER_THREAD; ++j) {
-            const int kk = c * U * 64 + scol[j] * 8;  // element offset in the row
-            v[j] = (sval[j] && kk < p.K) ? *(const uint4*)(srow[j] + (size_t)kk * 2) : make_uint4(0, 0, 0, 0);
+            const int kk = kbeg + c * U * 64 + scol[j] * 8;  // element offset in the row
+            v[j] = (sval[j] && kk < kend) ? *(const uint4*)(srow[j] + (size_t)kk * 2) : make_uint4(0, 0, 0, 0);
         }
     };
     auto stage_store = [&](int buf, const uint4 (&v)[PER_THREAD]) {
@@ -464,7 +469,7 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
         const int c0 = colw + b * 16;
         active[b] = c0 < p.ncols;  // blocks past the last column still stage and sync
         n[b] = min(c0, p.ncols - 16) + (lane & 15);
-        bptr[b] = BL::ptr(mat ? p.B1 : p.B0, e_off, n[b], p.K, kl);
+        bptr[b] = BL::ptr(mat ? p.B1 : p.B0, e_off, n[b], p.K, kbeg + kl);
         scl[b] = b_scale<WF>(S, s_off, n[b], p.K, 0);
     }
 
@@ -491,7 +496,7 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
                 for (int u = 0; u < U; ++u) {
                     const int ks = min(ks0 + u, nks - 1);
                     BL::load(bw[b][u], bptr[b], ks * 64);
-                    if constexpr (GROUPED) sg[b][u] = b_scale<WF>(S, s_off, n[b], p.K, ks * 64);
+                    if constexpr (GROUPED) sg[b][u] = b_scale<WF>(S, s_off, n[b], p.K, kbeg + ks * 64);
                     else sg[b][u] = scl[b];
                 }
             }
@@ -575,8 +580,12 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int r = row0 + rb * 16 + (lane >> 4) * 4 + i;
-                        if (r < seg_end)
-                            ((unsigned short*)p.out)[(long long)r * p.ldo + n[b]] = f32_to_bf16_rne(acc[b][rb][i]);
+                        if (r < seg_end) {
+                            if constexpr (EPI == EPI_F32)
+                                ((float*)p.out)[kz * p.split_stride + (long long)r * p.ldo + n[b]] = acc[b][rb][i];
+                            else
+                                ((unsigned short*)p.out)[(long long)r * p.ldo + n[b]] = f32_to_bf16_rne(acc[b][rb][i]);
+                        }
                     }
                 }
             }
@@ -590,16 +599,17 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
 // expert, which all read the same columns) then run together on one XCD and fetch those
 // weights from HBM once into its L2 instead of once per tile.
 template <int WF, int EPI, int U, int MAXRB, int NB>
-__global__ __launch_bounds__(256) void gemm_stream_kernel(GemmParams p, int ngroups) {
+__global__ __launch_bounds__(256) void gemm_stream_kernel(GemmParams p, int ngroups, int nsplit) {
     __shared__ uint4 As[2][16 * MAXRB * (U * 8 + 1)];
-    const int nt = *p.ntiles;
-    const int nitems = nt * ngroups;
+    const int nt = p.tile_seg == nullptr ? (p.nrows + 16 * MAXRB - 1) / (16 * MAXRB) : *p.ntiles;
+    const int nitems = nt * ngroups * nsplit;
     const int per_xcd = (nitems + 7) / 8;
     const int local = blockIdx.x / 8;
     if (local >= per_xcd) return;
     const int item = (blockIdx.x % 8) * per_xcd + local;
     if (item >= nitems) return;
-    stream_item<WF, EPI, U, MAXRB, NB>(p, item % nt, item / nt, As);
+    const int rest = item / nt;  // tile fastest, then column group, then K split
+    stream_item<WF, EPI, U, MAXRB, NB>(p, item % nt, rest % ngroups, rest / ngroups, As);
 }
 
 // ------------------------------------------------------------------ bf16, LDS-tiled form
@@ -677,7 +687,10 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     const int lane = t & 63;
     const int wave = t >> 6;
     const int wr = wave >> 3, wc = wave & 7;  // 2 x 8 wavefronts: 128 rows x 32 weight rows each
-    const int total = *p.ntiles * ncb;
+    // grouped: tiles from the tile table; dense (no table): 256-row tiles of nrows rows
+    const bool dense = p.tile_seg == nullptr;
+    const int ntl = dense ? (p.nrows + TBM - 1) / TBM : *p.ntiles;
+    const int total = ntl * ncb;
     const int per_xcd = (total + 7) / 8;
     const int local = blockIdx.x / 8;
     if (local >= per_xcd) return;
@@ -685,9 +698,9 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     if (item >= total) return;
     const int tile = item / ncb;
     const int cb = item % ncb;
-    const int e = p.tile_seg[tile];
-    const int row0 = p.tile_row0[tile];
-    const int seg_end = p.seg_start[e + 1];
+    const int e = dense ? 0 : p.tile_seg[tile];
+    const int row0 = dense ? tile * TBM : p.tile_row0[tile];
+    const int seg_end = dense ? p.nrows : p.seg_start[e + 1];
     // output columns: gate/up -> 128 columns (x2 matrices); down -> 256 columns
     const int n0 = SWIGLU ? cb * (TBN / 2) : cb * TBN;
     const int nks = p.K / TBK;
@@ -841,6 +854,12 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
                 const float up = round_bf16(acc[mb][1][i]);
                 const float sgl = round_bf16(silu(gt));
                 ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(sgl * up);
+            } else if constexpr (EPI == EPI_F32) {
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+                    const int n = n0 + wc * 32 + nb * 16 + (lane & 15);
+                    ((float*)p.out)[(long long)r * p.ldo + n] = acc[mb][nb][i];
+                }
             } else {
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) {
@@ -1101,12 +1120,22 @@ __global__ __launch_bounds__(256) void reduce_splits_kernel(const float* __restr
 
 // Streaming (decode) form: one (tile, column group) item per work-group; NB 16-column
 // blocks per wavefront.
-template <int EPI, int U, int NB>
-int stream_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, const char* name) {
+template <int EPI, int U, int NB, int MAXRB = 1>
+int stream_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, const char* name,
+                    int nsplit = 1) {
     const int ngroups = (EPI == EPI_SWIGLU) ? ceil_div(p.ncols, 32 * NB) : ceil_div(p.ncols, 64 * NB);
-    const long long items = 8LL * ceil_div(ntiles_max * ngroups, 8);
+    const long long items = 8LL * ceil_div(ntiles_max * ngroups * nsplit, 8);
     if (items <= 0) return YVMOE_OK;
-#define YV_ST(WFV) gemm_stream_kernel<WFV, EPI, U, 1, NB><<<(unsigned)items, 256, 0, st>>>(p, ngroups)
+#define YV_ST(WFV) gemm_stream_kernel<WFV, EPI, U, MAXRB, NB><<<(unsigned)items, 256, 0, st>>>(p, ngroups, nsplit)
+    if constexpr (EPI == EPI_F32) {  // dense fp32 output: bf16 weights only
+        if (wf != YVMOE_W_BF16) {
+            set_error("%s: fp32-output streaming form needs bf16 weights", name);
+            return YVMOE_ERR_DTYPE;
+        }
+        YV_ST(YVMOE_W_BF16);
+        YV_LAUNCH_CHECK(name);
+        return YVMOE_OK;
+    }
     switch (wf) {
         case YVMOE_W_BF16: YV_ST(YVMOE_W_BF16); break;
         case YVMOE_W_INT8: YV_ST(YVMOE_W_INT8); break;
@@ -1131,11 +1160,19 @@ int tile_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, c
     if (ntiles_max <= 0) return YVMOE_OK;
     const int ncb = p.ncols / cols;
     const long long blocks = 8LL * ceil_div(ntiles_max * ncb, 8);
-    switch (wf) {
-        case YVMOE_W_BF16: gemm_tile_kernel<YVMOE_W_BF16, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
-        case YVMOE_W_INT8: gemm_tile_kernel<YVMOE_W_INT8, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
-        case YVMOE_W_FP8: gemm_tile_kernel<YVMOE_W_FP8, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
-        default: set_error("%s: no tiled form for weight format %d", name, wf); return YVMOE_ERR_DTYPE;
+    if (EPI == EPI_F32 && (p.tile_seg != nullptr || wf != YVMOE_W_BF16)) {
+        set_error("%s: the fp32-output tiled form is dense with bf16 weights", name);
+        return YVMOE_ERR_UNSUPPORTED;
+    }
+    if constexpr (EPI == EPI_F32) {
+        gemm_tile_kernel<YVMOE_W_BF16, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb);
+    } else {
+        switch (wf) {
+            case YVMOE_W_BF16: gemm_tile_kernel<YVMOE_W_BF16, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
+            case YVMOE_W_INT8: gemm_tile_kernel<YVMOE_W_INT8, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
+            case YVMOE_W_FP8: gemm_tile_kernel<YVMOE_W_FP8, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
+            default: set_error("%s: no tiled form for weight format %d", name, wf); return YVMOE_ERR_DTYPE;
+        }
     }
     YV_LAUNCH_CHECK(name);
     return YVMOE_OK;
@@ -1194,6 +1231,11 @@ int dense_gemm_launch(const void* x, int act, int N, int K, const void* w, int n
     p.ldo = ld;
     p.nrows = N;
     const int wf = (act == YVMOE_ACT_F32) ? YVMOE_W_F32 : YVMOE_W_BF16;
+    if (dense_tiled(act, N, ncols, K)) {
+        p.kchunk = K;
+        p.out = out;
+        return tile_dispatch<EPI_F32>(wf, p, ceil_div(N, TBM), st, name);
+    }
     const int ks = dense_ksplit(N, ncols, K);
     const int ncb = (ncols % 32 == 0) ? 2 : 1;
     if (ks == 1 || partials == nullptr) {
@@ -1210,6 +1252,32 @@ int dense_gemm_launch(const void* x, int act, int N, int K, const void* w, int n
     reduce_splits_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(partials, ks, n, n, out);
     YV_LAUNCH_CHECK("dense_gemm_reduce");
     return YVMOE_OK;
+}
+
+int dense_partials_launch(const void* x, int act, int N, int K, const void* w, int ncols,
+                          float* out, int ld, hipStream_t st, const char* name) {
+    if (N <= 0) return YVMOE_OK;
+    GemmParams p{};
+    p.A = x;
+    p.lda = K;
+    p.rowmap = nullptr;
+    p.B0 = w;
+    p.K = K;
+    p.ncols = ncols;
+    p.ldo = ld;
+    p.nrows = N;
+    p.out = out;
+    p.split_stride = (long long)N * ld;
+    const int ks = dense_splits(act, N, ncols, K);
+    p.kchunk = K / ks;
+    if (dense_tiled(act, N, ncols, K)) return tile_dispatch<EPI_F32>(YVMOE_W_BF16, p, ceil_div(N, TBM), st, name);
+    if (dense_streamed(act, N, ncols, K)) {
+        if (N <= 16) return stream_dispatch<EPI_F32, 4, 1, 1>(YVMOE_W_BF16, p, 1, st, name, ks);
+        return stream_dispatch<EPI_F32, 2, 1, 4>(YVMOE_W_BF16, p, 1, st, name, ks);
+    }
+    const int wf = (act == YVMOE_ACT_F32) ? YVMOE_W_F32 : YVMOE_W_BF16;
+    return gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), (ncols % 32 == 0) ? 2 : 1, ks,
+                                  st, name);
 }
 
 int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, float* out, int ld,

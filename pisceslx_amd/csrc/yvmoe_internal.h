@@ -59,11 +59,33 @@ inline int router_ksplit(int N, int E, int act, int H) {
     return ks;
 }
 
+// Dense fp32-output GEMMs of more than 64 rows with bf16 operands, 256-multiple columns and
+// 64-multiple K run on the LDS-tiled MFMA form (256 x 256 output tiles, no K split).
+inline bool dense_tiled(int act, int N, int ncols, int K) {
+    return act == YVMOE_ACT_BF16 && N > 64 && ncols % 256 == 0 && K % 64 == 0;
+}
+
 // K splits of a dense fp32-output GEMM over ncols columns (same rule as the router's).
 inline int dense_ksplit(int N, int ncols, int K) {
     const int wgs = ceil_div(N > 0 ? N : 1, 64) * ceil_div(ncols, 64);
     int ks = 1;
     while (wgs * ks * 2 <= 512 && K % (ks * 2 * 64) == 0 && K / (ks * 2) >= 128) ks *= 2;
+    return ks;
+}
+
+// Dense fp32-output GEMMs of up to 64 rows with bf16 operands run on the weight-streaming
+// form (one 16- or 64-row tile, 64 columns per work-group), K split in two when that keeps
+// the work-groups at or below 1024: the weights are read once, the two partial sums are
+// summed by the consumer.
+inline bool dense_streamed(int act, int N, int ncols, int K) {
+    return act == YVMOE_ACT_BF16 && N <= 64 && ncols % 16 == 0 && K % 64 == 0;
+}
+inline int dense_splits(int act, int N, int ncols, int K) {
+    if (dense_tiled(act, N, ncols, K)) return 1;
+    if (!dense_streamed(act, N, ncols, K)) return dense_ksplit(N, ncols, K);
+    const int items = ceil_div(ncols, 64);
+    int ks = 1;
+    while (ks < 2 && items * ks * 2 <= 1024 && K % (ks * 2 * 64) == 0 && K / (ks * 2) >= 256) ks *= 2;
     return ks;
 }
 
@@ -158,13 +180,18 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
 // sums (when the rule splits) go to partials and are reduced in split order.
 int dense_gemm_launch(const void* x, int act, int N, int K, const void* w, int ncols, float* out,
                       int ld, float* partials, hipStream_t st, const char* name);
-// YvMoEGate logits and loss (yvmoe_moegate.hip). Workspace: heads GEMM output [N][Rh],
-// DG activations [N][dg_dim], split-K partial sums of either GEMM, per-work-group loss sums.
+// The same product left as dense_splits(act, N, ncols, K) partial sums: split z at
+// out + z * N * ld (its K range z * K / splits ...), for the consumer to sum in split order.
+int dense_partials_launch(const void* x, int act, int N, int K, const void* w, int ncols,
+                          float* out, int ld, hipStream_t st, const char* name);
+// YvMoEGate logits and loss (yvmoe_moegate.hip). Workspace: the projections [N][P] (DG
+// activations, then the heads), split-K partial sums, per-work-group loss sums.
 struct GateWs {
-    size_t heads, dg, partials, loss, bytes;
+    size_t proj, loss, bytes;
     int groups;
 };
 int moegate_heads_rows(const yvmoe_moegate* g);
+int moegate_proj_rows(const yvmoe_moegate* g);
 GateWs gate_ws(int N, int act, const yvmoe_moegate* g);
 int moegate_launch(const void* x, int act, int N, const yvmoe_moegate* g, const int* modal_id,
                    float* logits, float* loss, char* ws, hipStream_t st);

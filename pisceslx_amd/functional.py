@@ -209,12 +209,10 @@ class MoEGateState:
     sparsity_k: int
     n_modalities: int
     heads: int                      # _lib.HEAD_* bits
-    w_heads: torch.Tensor           # [Rh, H] activation dtype
-    w_dg: Optional[torch.Tensor]    # [dg, H] activation dtype
+    w_proj: torch.Tensor            # [(dg if HiCL) + Rh, H] activation dtype
     dg_bias: Optional[torch.Tensor]
     prototypes_t: Optional[torch.Tensor]
-    enc2_t: Optional[torch.Tensor]
-    expert_enc_t: Optional[torch.Tensor]
+    eo_mat: Optional[torch.Tensor]  # [D, E] fp32
     modal_affinity: Optional[torch.Tensor]
     expert_bias: Optional[torch.Tensor]
     w_hicl: float
@@ -230,16 +228,15 @@ class MoEGateState:
     capacity_loss: float
 
     def tensors(self):
-        return [t for t in (self.w_heads, self.w_dg, self.dg_bias, self.prototypes_t, self.enc2_t,
-                            self.expert_enc_t, self.modal_affinity, self.expert_bias)
+        return [t for t in (self.w_proj, self.dg_bias, self.prototypes_t, self.eo_mat,
+                            self.modal_affinity, self.expert_bias)
                 if t is not None]
 
     def struct(self) -> _lib.MoEGate:
         return _lib.MoEGate(
             self.num_experts, self.hidden, self.enc_dim, self.dg_dim, self.sparsity_k,
-            self.n_modalities, self.heads, 0, _ptr(self.w_heads), _ptr(self.w_dg),
-            _ptr(self.dg_bias), _ptr(self.prototypes_t), _ptr(self.enc2_t),
-            _ptr(self.expert_enc_t), _ptr(self.modal_affinity), _ptr(self.expert_bias),
+            self.n_modalities, self.heads, 0, _ptr(self.w_proj), _ptr(self.dg_bias), _ptr(self.prototypes_t), _ptr(self.eo_mat),
+            _ptr(self.modal_affinity), _ptr(self.expert_bias),
             self.w_hicl, self.w_got, self.w_soft, self.w_eo, self.soft_temperature,
             self.temperature, self.soft_eps, self.load_balance_alpha, self.z_loss_alpha,
             self.soft_budget, self.capacity_loss, 0.0)

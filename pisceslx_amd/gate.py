@@ -301,24 +301,28 @@ class YvMoEGate(nn.Module):
         for name, bit in self.HEAD_NAMES:
             if name not in self._pruned_heads:
                 heads |= bit
+        enc = self.hicl_dg_encoder
         with torch.no_grad():
             dev = self.gate.weight.device
-            rh = (4 * E + D + 15) // 16 * 16
-            w_heads = torch.zeros(rh, H, dtype=wdt, device=dev)
-            w_heads[0:E] = self.gate.weight
-            w_heads[E:2 * E] = self.got_cluster_proj.weight
-            w_heads[2 * E:3 * E] = self.gate_k.weight
-            w_heads[3 * E:4 * E] = self.gate_v.weight
-            w_heads[4 * E:4 * E + D] = self.input_encoder[0].weight
-            enc = self.hicl_dg_encoder
-            w_dg = enc.dg_proj.weight.detach().to(wdt).contiguous()
+            # [dg_proj (with HiCL); gate; got_cluster_proj; gate_k; gate_v; input_encoder.0; 0]
+            dg = enc.dg_dim if heads & _lib.HEAD_HICL else 0
+            rh = (4 * E + D + 255) // 256 * 256
+            w_proj = torch.zeros(dg + rh, H, dtype=wdt, device=dev)
+            if dg:
+                w_proj[:dg] = enc.dg_proj.weight
+            w_proj[dg:dg + E] = self.gate.weight
+            w_proj[dg + E:dg + 2 * E] = self.got_cluster_proj.weight
+            w_proj[dg + 2 * E:dg + 3 * E] = self.gate_k.weight
+            w_proj[dg + 3 * E:dg + 4 * E] = self.gate_v.weight
+            w_proj[dg + 4 * E:dg + 4 * E + D] = self.input_encoder[0].weight
             dg_bias = enc.dg_bias.detach().float().contiguous()
             proto_t = self.hicl_prototypes.detach().float().t().contiguous()
-            enc2_t = self.input_encoder[2].weight.detach().float().t().contiguous()
+            # Expert-Oriented: silu(enc0 x) · enc2ᵀ · eeᵀ with ee = cap2(silu(cap0(emb))), a
+            # constant of the weights; both linear maps after the SiLU fold into one [D, E]
             cap0 = self.expert_capability_encoder[0].weight.detach().double()
             cap2 = self.expert_capability_encoder[2].weight.detach().double()
             ee = F.silu(self.expert_embeddings.detach().double() @ cap0.t()) @ cap2.t()
-            eenc_t = ee.t().float().contiguous()
+            eo_mat = (self.input_encoder[2].weight.detach().double().t() @ ee.t()).float().contiguous()
             modal = self.expert_modal_affinity.detach().float().contiguous()
             ebias = self.expert_bias.detach().float().contiguous()
         temp, cap_loss = self._host_constants(seq_len)
@@ -328,7 +332,7 @@ class YvMoEGate(nn.Module):
                                if hasattr(self, name) else 0.0)
         self._state = yvf.MoEGateState(
             E, H, D, enc.dg_dim, min(enc.sparsity_k, enc.dg_dim), self.n_modalities, heads,
-            w_heads, w_dg, dg_bias, proto_t, enc2_t, eenc_t, modal, ebias,
+            w_proj, dg_bias, proto_t, eo_mat, modal, ebias,
             scalar("w_hicl"), scalar("w_got"), scalar("w_soft"),
             scalar("w_expert_orient"), float(self.soft_moe_temperature), temp, soft_eps,
             float(self.load_balance_alpha), float(self.z_loss_alpha),

@@ -6,7 +6,8 @@ against the C routing oracle given the GPU's logits (indices, weights, counts, p
 ``top_scores`` are those weights in x's dtype, and the loss is within 1e-4 relative of the
 oracle's. Cases: the decode shape of the 7B-style layer (hidden 4096, 64 experts, top-6,
 64 tokens), a prefill sample, heads weighted up so every head moves the logits by O(1), exact
-ties at the 32nd DG activation, fewer than 32 positive DG activations, modal ids, a pruned
+ties at the 32nd DG activation, more candidates than the ranking takes (exact radix
+select), fewer than 32 positive DG activations, modal ids, a pruned
 head, the long-sequence temperature, fp32 activations, N = 0, determinism, and the PathMoE
 stage cache.
 """
@@ -97,6 +98,29 @@ def test_dg_ties_and_few_positives(cuda, oracle):
     _check(g, x, oracle)
     with torch.no_grad():                   # none positive: HiCL adds 0
         dg.dg_bias.fill_(-1.0)
+    _check(g, x, oracle)
+
+
+def test_dg_exact_select_beyond_candidates(cuda, oracle):
+    H, E = 1024, 8                          # DG width 4096
+    g = _gate(H, E, 2, scale_heads=True, seed=3)
+    dg = g.hicl_dg_encoder
+    x = torch.randn(2, 5, H, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16).cuda()
+    with torch.no_grad():                   # ~1500 candidates tie at the bound: exact select
+        dg.dg_proj.weight.zero_()
+        b = torch.full((dg.dg_dim,), -1.0)
+        b[torch.arange(1, 1001, 2)] = 1.0
+        b[torch.arange(2, 3002, 3)] = 1.0
+        b[[17, 900, 40, 3]] = torch.tensor([2.0, 3.0, 2.5, 2.0])
+        dg.dg_bias.copy_(b)
+    _check(g, x, oracle)
+    with torch.no_grad():                   # every activation equal
+        dg.dg_bias.fill_(0.5)
+    _check(g, x, oracle)
+    with torch.no_grad():                   # 2000 distinct values above the bound
+        b = torch.full((dg.dg_dim,), -1.0)
+        b[1000:3000] = 1.0 + torch.arange(2000) * 1e-3
+        dg.dg_bias.copy_(b)
     _check(g, x, oracle)
 
 
