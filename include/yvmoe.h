@@ -263,6 +263,22 @@ int32_t yvmoe_moegate_logits(const void* x, int32_t act_dtype, int32_t n_tokens,
                              const yvmoe_moegate* gate, const int32_t* modal_id, float* logits,
                              float* loss, void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * The whole eval forward of YvMoEGate (gate.py:310-451 without the PathMoE cache, which is
+ * module state): yvmoe_moegate_logits, then the top-k routing of the logits (softmax, top_k,
+ * softmax of the k scores, gate.py:393, :414-416) into `routing` (fixed mode: capacity -1),
+ * with the expert counts, offsets and permutation of yvmoe_route.
+ * workspace: at least yvmoe_moegate_forward_workspace_bytes(); the routing region sits at its
+ * start, where yvmoe_expert_ffn expects it, so the same workspace can be handed to
+ * yvmoe_expert_ffn next.
+ */
+size_t yvmoe_moegate_forward_workspace_bytes(int32_t n_tokens, int32_t act_dtype, int32_t top_k,
+                                             const yvmoe_moegate* gate);
+int32_t yvmoe_moegate_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
+                              const yvmoe_moegate* gate, const int32_t* modal_id, int32_t top_k,
+                              float* logits, float* loss, yvmoe_routing* routing,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -48,6 +48,8 @@ EXPORTED_SYMBOLS = (
     "yvmoe_forward",
     "yvmoe_moegate_workspace_bytes",
     "yvmoe_moegate_logits",
+    "yvmoe_moegate_forward_workspace_bytes",
+    "yvmoe_moegate_forward",
 )
 
 # YvMoEGate auxiliary heads (YVMOE_HEAD_*)
@@ -161,6 +163,11 @@ def _declare(l: ctypes.CDLL) -> None:
     l.yvmoe_moegate_workspace_bytes.argtypes = [i32, i32, ctypes.POINTER(MoEGate)]
     l.yvmoe_moegate_logits.restype = i32
     l.yvmoe_moegate_logits.argtypes = [vp, i32, i32, ctypes.POINTER(MoEGate), vp, vp, vp, vp, sz, vp]
+    l.yvmoe_moegate_forward_workspace_bytes.restype = sz
+    l.yvmoe_moegate_forward_workspace_bytes.argtypes = [i32, i32, i32, ctypes.POINTER(MoEGate)]
+    l.yvmoe_moegate_forward.restype = i32
+    l.yvmoe_moegate_forward.argtypes = [vp, i32, i32, ctypes.POINTER(MoEGate), vp, i32, vp, vp,
+                                        ctypes.POINTER(Routing), vp, sz, vp]
     l.yvmoe_forward.restype = i32
     l.yvmoe_forward.argtypes = [vp, i32, i32, ctypes.POINTER(Router), ctypes.POINTER(ExpertWeights),
                                 vp, vp, vp, vp, ctypes.POINTER(Routing), vp, sz, vp]

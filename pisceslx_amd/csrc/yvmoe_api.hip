@@ -308,4 +308,45 @@ int32_t yvmoe_moegate_logits(const void* x, int32_t act_dtype, int32_t n_tokens,
                           (hipStream_t)stream);
 }
 
+size_t yvmoe_moegate_forward_workspace_bytes(int32_t n_tokens, int32_t act_dtype, int32_t top_k,
+                                             const yvmoe_moegate* gate) {
+    if (n_tokens < 0 || check_moegate(gate, act_dtype) != YVMOE_OK) return 0;
+    if (top_k < 1 || top_k > YVMOE_MAX_TOPK || top_k > gate->num_experts) return 0;
+    return route_ws(n_tokens, gate->num_experts, top_k).bytes + gate_ws(n_tokens, act_dtype, gate).bytes;
+}
+
+int32_t yvmoe_moegate_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
+                              const yvmoe_moegate* gate, const int32_t* modal_id, int32_t top_k,
+                              float* logits, float* loss, yvmoe_routing* routing,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = check_moegate(gate, act_dtype);
+    if (rc) return rc;
+    rc = check_routing(routing, n_tokens);
+    if (rc) return rc;
+    const int E = gate->num_experts;
+    YV_REQUIRE(top_k >= 1 && top_k <= YVMOE_MAX_TOPK && top_k <= E, YVMOE_ERR_SHAPE,
+               "top_k=%d outside [1, min(E=%d, %d)]", top_k, E, YVMOE_MAX_TOPK);
+    YV_REQUIRE(n_tokens >= 0, YVMOE_ERR_ARG, "n_tokens=%d < 0", n_tokens);
+    YV_REQUIRE(loss != nullptr, YVMOE_ERR_ARG, "loss is NULL");
+    YV_REQUIRE(n_tokens == 0 || (x && logits), YVMOE_ERR_ARG, "NULL pointer");
+    YV_REQUIRE(modal_id == nullptr || (gate->modal_affinity && gate->n_modalities > 0),
+               YVMOE_ERR_ARG, "modal_id needs modal_affinity");
+    YV_REQUIRE((long long)n_tokens * top_k < (1ll << 31), YVMOE_ERR_SHAPE, "N*k overflows int32");
+    const size_t rbytes = route_ws(n_tokens, E, top_k).bytes;
+    const size_t need = rbytes + gate_ws(n_tokens, act_dtype, gate).bytes;
+    YV_REQUIRE(workspace != nullptr && workspace_bytes >= need, YVMOE_ERR_WORKSPACE,
+               "workspace %zu bytes, need %zu", workspace_bytes, need);
+    hipStream_t st = (hipStream_t)stream;
+    char* ws = (char*)workspace;
+    rc = moegate_launch(x, act_dtype, n_tokens, gate, modal_id, logits, loss, ws + rbytes, st);
+    if (rc) return rc;
+    yvmoe_router r{};
+    r.num_experts = E;
+    r.hidden = gate->hidden;
+    r.top_k = top_k;
+    r.fixed_shape_mode = 1;
+    return route_launch(n_tokens > 0 ? logits : nullptr, E, nullptr, E, n_tokens, &r, -1, routing, ws, st);
+}
+
 }  // extern "C"

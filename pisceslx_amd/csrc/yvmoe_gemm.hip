@@ -69,7 +69,14 @@ struct GemmParams {
     int nrows;  // rows when there is no tile table
     int kchunk;              // K range of one split (multiple of 64); K when not split
     long long split_stride;  // output elements between splits (EPI_F32 partial sums)
+    const float* col_bias;   // EPI_F32: added to columns < col_bias_n by split 0 (or NULL)
+    int col_bias_n;
 };
+
+// EPI_F32 output value of column n for split kz: the accumulator plus the column bias.
+__device__ __forceinline__ float f32_out(const GemmParams& p, float acc, int n, int kz) {
+    return (p.col_bias != nullptr && kz == 0 && n < p.col_bias_n) ? acc + p.col_bias[n] : acc;
+}
 
 // Round-to-nearest-even fp32 -> bf16 pair (v_cvt_pk_bf16_f32), lo in bits 0..15.
 __device__ __forceinline__ unsigned pack_bf16(float lo, float hi) {
@@ -371,7 +378,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
                     if (r < seg_end) {
                         if constexpr (EPI == EPI_F32) {
                             ((float*)p.out)[blockIdx.z * p.split_stride + (long long)r * p.ldo + n] =
-                                acc[0][cb][rb][i];
+                                f32_out(p, acc[0][cb][rb][i], n, blockIdx.z);
                         } else if constexpr (EPI == EPI_SWIGLU) {
                             const float g = round_bf16(acc[0][cb][rb][i]);
                             const float u = round_bf16(acc[NM - 1][cb][rb][i]);
@@ -582,7 +589,8 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
                         const int r = row0 + rb * 16 + (lane >> 4) * 4 + i;
                         if (r < seg_end) {
                             if constexpr (EPI == EPI_F32)
-                                ((float*)p.out)[kz * p.split_stride + (long long)r * p.ldo + n[b]] = acc[b][rb][i];
+                                ((float*)p.out)[kz * p.split_stride + (long long)r * p.ldo + n[b]] =
+                                    f32_out(p, acc[b][rb][i], n[b], kz);
                             else
                                 ((unsigned short*)p.out)[(long long)r * p.ldo + n[b]] = f32_to_bf16_rne(acc[b][rb][i]);
                         }
@@ -858,7 +866,7 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) {
                     const int n = n0 + wc * 32 + nb * 16 + (lane & 15);
-                    ((float*)p.out)[(long long)r * p.ldo + n] = acc[mb][nb][i];
+                    ((float*)p.out)[(long long)r * p.ldo + n] = f32_out(p, acc[mb][nb][i], n, 0);
                 }
             } else {
 #pragma unroll
@@ -955,6 +963,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
                     if (r < seg_end) {
                         float v;
                         if constexpr (EPI == EPI_SWIGLU) v = silu(acc[0][cb][rb][i]) * acc[NM - 1][cb][rb][i];
+                        else if constexpr (EPI == EPI_F32) v = f32_out(p, acc[0][cb][rb][i], n, blockIdx.z);
                         else v = acc[0][cb][rb][i];
                         ((float*)p.out)[blockIdx.z * p.split_stride + (long long)r * p.ldo + n] = v;
                     }
@@ -1255,9 +1264,12 @@ int dense_gemm_launch(const void* x, int act, int N, int K, const void* w, int n
 }
 
 int dense_partials_launch(const void* x, int act, int N, int K, const void* w, int ncols,
-                          float* out, int ld, hipStream_t st, const char* name) {
+                          float* out, int ld, const float* col_bias, int col_bias_n,
+                          hipStream_t st, const char* name) {
     if (N <= 0) return YVMOE_OK;
     GemmParams p{};
+    p.col_bias = col_bias;
+    p.col_bias_n = col_bias_n;
     p.A = x;
     p.lda = K;
     p.rowmap = nullptr;

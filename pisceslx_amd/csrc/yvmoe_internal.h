@@ -181,9 +181,11 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
 int dense_gemm_launch(const void* x, int act, int N, int K, const void* w, int ncols, float* out,
                       int ld, float* partials, hipStream_t st, const char* name);
 // The same product left as dense_splits(act, N, ncols, K) partial sums: split z at
-// out + z * N * ld (its K range z * K / splits ...), for the consumer to sum in split order.
+// out + z * N * ld (its K range z * K / splits ...), for the consumer to sum in split order;
+// split 0 also adds col_bias[n] to columns n < col_bias_n (col_bias may be NULL).
 int dense_partials_launch(const void* x, int act, int N, int K, const void* w, int ncols,
-                          float* out, int ld, hipStream_t st, const char* name);
+                          float* out, int ld, const float* col_bias, int col_bias_n,
+                          hipStream_t st, const char* name);
 // YvMoEGate logits and loss (yvmoe_moegate.hip). Workspace: the projections [N][P] (DG
 // activations, then the heads), split-K partial sums, per-work-group loss sums.
 struct GateWs {

@@ -22,10 +22,7 @@
 namespace yvmoe {
 namespace {
 
-constexpr int kGateNT = 1024;      // threads of the per-token kernel
-constexpr int kGateMaxV = 32;      // DG activations per thread, held in registers (dg <= 32768)
 constexpr int kGateMaxSel = 64;    // most DG entries kept per token
-constexpr int kGateCand = 1024;    // most candidates ranked directly (else radix select)
 constexpr int kGateGroups = 1024;  // work-groups of the per-token kernel (fixed for a given N)
 // Buffer resource word 3 for raw 32-bit buffer loads (data format 32, no swizzle).
 constexpr int kBufferFormat = 0x00020000;
@@ -54,15 +51,37 @@ struct GateArgs {
     float* part;  // [E + 2][G]
 };
 
+// Rotation by O lanes inside each row of 16 lanes (DPP row_ror).
+template <int O>
+__device__ __forceinline__ float ror16(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + O, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float lane_of(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+// Wave sum / max, the same value in every lane: rotations by 8, 4, 2, 1 inside each row (each
+// step adds two values that the partner lane adds in the other order, so all 16 lanes of a
+// row agree bit for bit), then the four row results in row order.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-    return v;
+    v = v + ror16<8>(v);
+    v = v + ror16<4>(v);
+    v = v + ror16<2>(v);
+    v = v + ror16<1>(v);
+    return ((lane_of(v, 0) + lane_of(v, 16)) + lane_of(v, 32)) + lane_of(v, 48);
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-    return v;
+    v = fmaxf(v, ror16<8>(v));
+    v = fmaxf(v, ror16<4>(v));
+    v = fmaxf(v, ror16<2>(v));
+    v = fmaxf(v, ror16<1>(v));
+    return fmaxf(fmaxf(lane_of(v, 0), lane_of(v, 16)), fmaxf(lane_of(v, 32), lane_of(v, 48)));
+}
+// Maximum over each row of 16 lanes.
+__device__ __forceinline__ float row_max(float v) {
+    v = fmaxf(v, ror16<8>(v));
+    v = fmaxf(v, ror16<4>(v));
+    v = fmaxf(v, ror16<2>(v));
+    return fmaxf(v, ror16<1>(v));
 }
 
 // Work-group sum / max; every thread gets the same value (fixed order: lanes by xor
@@ -152,7 +171,7 @@ __device__ __forceinline__ unsigned wave_prefix_sum(unsigned v) {
     return v;
 }
 
-// Exact radix select over the kGateMaxV keys each thread holds (key(j) == 0: not counted):
+// Exact radix select over the JV keys each thread holds (key(j) == 0: not counted):
 // the R-th largest key, in 11/11/10-bit digits. A pass ends early when the bin holding the
 // R-th key is counted whole. Result: found = false if fewer than R keys are counted (all of
 // them are then taken); else every key > T is taken and, when !whole, the `need` ... of the
@@ -161,7 +180,7 @@ struct RadixPick {
     unsigned T, need;
     bool found, whole;
 };
-template <int NT, class KeyFn>
+template <int NT, int JV, class KeyFn>
 __device__ RadixPick radix_select(KeyFn key, unsigned R, unsigned* hist, unsigned* ctl) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     RadixPick rp{0u, R, true, false};
@@ -173,7 +192,7 @@ __device__ RadixPick radix_select(KeyFn key, unsigned R, unsigned* hist, unsigne
         for (int b = tid; b < nb + nb / 32; b += NT) hist[b] = 0u;
         __syncthreads();
 #pragma unroll
-        for (int j = 0; j < kGateMaxV; ++j) {
+        for (int j = 0; j < JV; ++j) {
             const unsigned k = key(j);
             if (k != 0u && (k & hmask) == prefix) atomicAdd(&hist[hpad((int)((k >> sh) & (unsigned)(nb - 1)))], 1u);
         }
@@ -219,89 +238,147 @@ __device__ RadixPick radix_select(KeyFn key, unsigned R, unsigned* hist, unsigne
 }
 
 // Per token: the DG activations stay in registers (kGateMaxV per thread, 16-byte loads:
-// register 4 j4 + c holds index 4 (tid + NT j4) + c). Selection of the sel_k largest:
-//   1. a lower bound: the sel_k-th largest of the 64 maxima of 16-lane groups (sel_k groups
-//      each hold an element at least that large, so every kept element passes it);
+// register 4 j4 + c holds index 4 (tid + NT j4) + c). Every load that does not depend on the
+// selection — the head columns, the expert bias and modal affinity, the expert-oriented
+// matrix — is issued with the row loads, so a token waits on global memory twice: the rows,
+// then the prototype gathers of the kept entries. Selection of the sel_k largest:
+//   1. a lower bound: the sel_k-th largest of the NT / 16 maxima of 16-lane groups (sel_k
+//      groups each hold an element at least that large, so every kept element passes it);
 //   2. the elements at or above the bound are appended to a candidate list (typically a few
-//      dozen); if more than kGateCand pass, an exact radix select over the float bit
-//      patterns (non-negative floats order like their bits) picks the sel_k instead, with a
-//      second select over the indices when the sel_k-th value is tied;
+//      dozen); if more than NT pass, an exact radix select over the float bit patterns
+//      (non-negative floats order like their bits) picks the sel_k instead, with a second
+//      select over the indices when the sel_k-th value is tied;
 //   3. each candidate's rank in (value descending, index ascending) order places it: ranks
 //      below sel_k are kept, in that order (ties at the threshold keep the lower indices).
-template <int NT, int NS>
+template <int NT, int NS, int J4>
 __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
-    constexpr int Q = NT / 256;  // threads per output of the split dot products
-    constexpr int NGRP = NT / 16;
-    constexpr int J4 = kGateMaxV / 4;
-    static_assert(NT == 1024, "the split dot products assume 4 x 256 threads");
-    static_assert(kGateCand <= NT && kGateMaxSel <= NGRP && kGateMaxSel <= 64, "sizes");
+    constexpr int Q = NT / 256;    // threads per output of the split dot products
+    constexpr int NGRP = NT / 16;  // 16-lane groups of the lower bound (sel_k <= NGRP)
+    constexpr int CAND = NT;       // most candidates ranked directly (else radix select)
+    constexpr int JV = 4 * J4;     // DG activations per thread
+    constexpr int EOP = 64 / Q;    // expert-oriented terms prefetched per thread (d < 64)
+    static_assert(NT == 512 || NT == 1024, "512 or 1024 threads");
     __shared__ unsigned hist[2048 + 64];
-    __shared__ float cand_val[kGateCand];
-    __shared__ int cand_idx[kGateCand];
+    __shared__ float cand_val[CAND];
+    __shared__ int cand_idx[CAND];
     __shared__ float sel_val[kGateMaxSel];
     __shared__ int sel_idx[kGateMaxSel];
     __shared__ float gmax[NGRP];
     __shared__ float s_lk[YVMOE_MAX_EXPERTS];
     __shared__ float s_h[256];
-    __shared__ float s_part[Q][256];
+    __shared__ float s_ph[Q][256];  // HiCL dot partial sums
+    __shared__ float s_pe[Q][256];  // expert-oriented dot partial sums
     __shared__ float red[2][NT / 64];
     __shared__ unsigned ctl[8];
     __shared__ float s_med, s_tlb;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = a.E, D = a.D, K = a.sel_k;
     const bool is_e = tid < E;
+    const bool hicl_on = (a.mask & YVMOE_HEAD_HICL) != 0;
+    const bool eo_on = (a.mask & YVMOE_HEAD_EO) != 0;
     const int o = tid & 255, q = tid >> 8;  // output and part of the split dot products
     float acc_score = 0.f, acc_z = 0.f, acc_soft = 0.f;
 
     for (int t = blockIdx.x; t < a.N; t += gridDim.x) {
         const float* hrow = a.heads + (long long)t * a.ld;
-        // ---------------------------------------------------------------- HiCL
-        float hicl = 0.f;
-        if (a.mask & YVMOE_HEAD_HICL) {
+        // thread coordinates made opaque per token: keeps the compiler from hoisting every
+        // loop-invariant address out of the token loop (and spilling them)
+        int tt = tid;
+        asm volatile("" : "+v"(tt));
+        const int ot = tt & 255, qt = tt >> 8;
+        // ---------------------------------------------------------------- loads
+        // head columns (split partial sums in order), bias terms, expert-oriented matrix
+        float gate = 0.f, got = 0.f, lk = 0.f, lv = 0.f, bias_e = 0.f;
+        if (is_e) {
+            gate = hrow[tt];
+            got = hrow[E + tt];
+            lk = hrow[2 * E + tt];
+            lv = hrow[3 * E + tt];
+#pragma unroll
+            for (int z = 1; z < NS; ++z) {
+                const float* hz = hrow + z * a.sstride;
+                gate += hz[tt];
+                got += hz[E + tt];
+                lk += hz[2 * E + tt];
+                lv += hz[3 * E + tt];
+            }
+            if (a.ebias != nullptr) bias_e = a.ebias[tt];
+        }
+        float h1 = 0.f;
+        if (eo_on && tid < D) {
+            h1 = hrow[4 * E + tt];
+#pragma unroll
+            for (int z = 1; z < NS; ++z) h1 += hrow[z * a.sstride + 4 * E + tt];
+        }
+        float em[EOP];  // eo_mat[d][o] for d = q + Q i < 64 (the rest is read at the dot)
+        if (eo_on) {
+            const float* ecol = a.eo_mat + ot;
+#pragma unroll
+            for (int i = 0; i < EOP; ++i) {
+                const int d = qt + Q * i;
+                em[i] = (o < E && d < D) ? ecol[d * E] : 0.f;
+            }
+        }
+        float v[JV];
+        if (hicl_on) {
             // Buffer loads bounded by the row length: offsets past the row read 0 (on gfx950
             // the range check covers the scalar offset too; rows are whole 1 KB blocks, so a
-            // 16-byte load is all in or all out), relu'd to 0 and never kept. The split partial
-            // sums are all loaded before any is added (in split order).
-            float v[kGateMaxV];
-            {
-                u32x4 raw[NS][J4];
+            // 16-byte load is all in or all out). Split 0 already holds dg_bias; relu follows
+            // the sum of the splits (in split order).
+            u32x4 raw[NS][J4];
 #pragma unroll
-                for (int z = 0; z < NS; ++z) {
-                    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-                        (void*)(a.dg + z * a.sstride + (long long)t * a.ld), 0, a.dgdim * 4, kBufferFormat);
+            for (int z = 0; z < NS; ++z) {
+                const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+                    (void*)(a.dg + z * a.sstride + (long long)t * a.ld), 0, a.dgdim * 4, kBufferFormat);
 #pragma unroll
-                    for (int j4 = 0; j4 < J4; ++j4)
-                        raw[z][j4] = __builtin_amdgcn_raw_buffer_load_b128(r, tid * 16, NT * 16 * j4, 0);
-                }
-                const __amdgpu_buffer_rsrc_t rb =
-                    __builtin_amdgcn_make_buffer_rsrc((void*)a.dg_bias, 0, a.dgdim * 4, kBufferFormat);
+                for (int j4 = 0; j4 < J4; ++j4)
+                    raw[z][j4] = __builtin_amdgcn_raw_buffer_load_b128(r, tt * 16, NT * 16 * j4, 0);
+            }
 #pragma unroll
-                for (int j4 = 0; j4 < J4; ++j4) {
-                    const u32x4 bias = __builtin_amdgcn_raw_buffer_load_b128(rb, tid * 16, NT * 16 * j4, 0);
+            for (int j4 = 0; j4 < J4; ++j4) {
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        float d = __uint_as_float(raw[0][j4][c]);
+                for (int c = 0; c < 4; ++c) {
+                    float d = __uint_as_float(raw[0][j4][c]);
 #pragma unroll
-                        for (int z = 1; z < NS; ++z) d += __uint_as_float(raw[z][j4][c]);
-                        d += __uint_as_float(bias[c]);
-                        v[4 * j4 + c] = d > 0.f ? d : 0.f;  // +0 for relu'd entries: bit pattern 0
-                    }
+                    for (int z = 1; z < NS; ++z) d += __uint_as_float(raw[z][j4][c]);
+                    v[4 * j4 + c] = d > 0.f ? d : 0.f;  // +0 for relu'd entries: bit pattern 0
                 }
             }
+        }
+        if (is_e) s_lk[tid] = lk;
+        if (eo_on && tid < D) s_h[tid] = h1 / (1.f + expf(-h1));  // SiLU
+        float modal_e = 0.f;  // affinity of this token's modality (gate.py:369-376)
+        if (is_e && a.modal_id != nullptr) {
+            const int md = a.modal_id[t];
+            if (md >= 0 && md < a.nmod) modal_e = a.modal[tt * a.nmod + md];
+        }
+        __syncthreads();
+        // ---------------------------------------------------------------- Expert-Oriented
+        // silu(input_encoder.0 x) · M with M = input_encoder.2ᵀ · encoded_expertsᵀ [D][E]
+        if (eo_on) {
+            float sum = 0.f;
+#pragma unroll
+            for (int i = 0; i < EOP; ++i) {
+                const int d = q + Q * i;
+                if (d < D) sum += s_h[d] * em[i];
+            }
+            if (o < E)
+                for (int d = 64 + q; d < D; d += Q) sum += s_h[d] * a.eo_mat[d * E + ot];
+            s_pe[q][o] = sum;
+        }
+        // ---------------------------------------------------------------- HiCL
+        if (hicl_on) {
 #define u(j) __float_as_uint(v[j])
-            int tid_v = tid;  // opaque per token: keeps the indices from being hoisted
-            asm volatile("" : "+v"(tid_v));
-#define IDX(j) (4 * (tid_v + NT * ((j) >> 2)) + ((j) & 3))
+#define IDX(j) (4 * (tt + NT * ((j) >> 2)) + ((j) & 3))
             // 1. lower bound from the 16-lane group maxima
             float m = 0.f;
 #pragma unroll
-            for (int j = 0; j < kGateMaxV; ++j) m = fmaxf(m, v[j]);
-#pragma unroll
-            for (int w = 8; w > 0; w >>= 1) m = fmaxf(m, __shfl_xor(m, w, 16));
+            for (int j = 0; j < JV; ++j) m = fmaxf(m, v[j]);
+            m = row_max(m);
             if ((lane & 15) == 0) gmax[tid >> 4] = m;
             __syncthreads();
             if (wave == 0) {
-                const float mv = gmax[lane];
+                const float mv = lane < NGRP ? gmax[lane] : 0.f;
                 const int mvb = __float_as_int(mv);
                 unsigned r = 0u;
 #pragma unroll 8
@@ -309,17 +386,17 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
                     const float g = __int_as_float(__builtin_amdgcn_readlane(mvb, k));
                     r += (g > mv || (g == mv && k < lane)) ? 1u : 0u;
                 }
-                if (r == (unsigned)(K - 1)) s_tlb = mv;
+                if (lane < NGRP && r == (unsigned)(K - 1)) s_tlb = mv;
                 if (lane == 0) ctl[5] = 0u;
             }
             __syncthreads();
             const unsigned tlb = __float_as_uint(s_tlb);
             // 2. candidates
 #pragma unroll
-            for (int j = 0; j < kGateMaxV; ++j) {
+            for (int j = 0; j < JV; ++j) {
                 if (u(j) != 0u && u(j) >= tlb) {
                     const unsigned slot = atomicAdd(&ctl[5], 1u);
-                    if (slot < (unsigned)kGateCand) {
+                    if (slot < (unsigned)CAND) {
                         cand_val[slot] = v[j];
                         cand_idx[slot] = IDX(j);
                     }
@@ -327,24 +404,24 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
             }
             __syncthreads();
             int C = (int)ctl[5];
-            if (C > kGateCand) {
+            if (C > CAND) {
                 __syncthreads();  // every thread has read C: ctl is reused
-                const RadixPick rv = radix_select<NT>([&](int j) { return u(j); }, (unsigned)K, hist, ctl);
+                const RadixPick rv = radix_select<NT, JV>([&](int j) { return u(j); }, (unsigned)K, hist, ctl);
                 unsigned ti = 0u;  // ties at the K-th value: the `need` lowest indices
                 if (rv.found && !rv.whole)
-                    ti = radix_select<NT>([&](int j) { return u(j) == rv.T ? 32768u - (unsigned)IDX(j) : 0u; },
+                    ti = radix_select<NT, JV>([&](int j) { return u(j) == rv.T ? 32768u - (unsigned)IDX(j) : 0u; },
                                           rv.need, hist, ctl).T;
                 if (tid == 0) ctl[5] = 0u;
                 __syncthreads();
 #pragma unroll
-                for (int j = 0; j < kGateMaxV; ++j) {
+                for (int j = 0; j < JV; ++j) {
                     bool take;
                     if (!rv.found) take = u(j) != 0u;
                     else if (rv.whole) take = u(j) >= rv.T;
                     else take = u(j) > rv.T || (u(j) == rv.T && 32768u - (unsigned)IDX(j) >= ti);
                     if (take) {
                         const unsigned slot = atomicAdd(&ctl[5], 1u);
-                        if (slot < (unsigned)kGateCand) {
+                        if (slot < (unsigned)CAND) {
                             cand_val[slot] = v[j];
                             cand_idx[slot] = IDX(j);
                         }
@@ -397,10 +474,11 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
             float h = 0.f;
             if (o < E) {
                 float pv[kGateMaxSel / Q];  // gathers issued together
+                const float* pcol = a.proto_t + ot;
 #pragma unroll
                 for (int i = 0; i < kGateMaxSel / Q; ++i) {
                     const int s = q + Q * i;
-                    pv[i] = s < nsel ? a.proto_t[(long long)sel_idx[s] * E + o] : 0.f;
+                    pv[i] = s < nsel ? pcol[(long long)sel_idx[s] * E] : 0.f;
                 }
 #pragma unroll
                 for (int i = 0; i < kGateMaxSel / Q; ++i) {
@@ -408,68 +486,33 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
                     if (s < nsel) h += sel_val[s] * pv[i];
                 }
             }
-            s_part[q][o] = h;
-            __syncthreads();
-            if (is_e) hicl = ((s_part[0][tid] + s_part[1][tid]) + s_part[2][tid]) + s_part[3][tid];
-        }
-        // ---------------------------------------------------------------- projection heads
-        auto hsum = [&](int i) {  // head column i, split partial sums in order
-            float sum = hrow[i];
-#pragma unroll
-            for (int z = 1; z < NS; ++z) sum += hrow[z * a.sstride + i];
-            return sum;
-        };
-        float gate = 0.f, got = 0.f, lk = 0.f, lv = 0.f;
-        if (is_e) {
-            gate = hsum(tid);
-            got = hsum(E + tid);
-            lk = hsum(2 * E + tid);
-            lv = hsum(3 * E + tid);
-            s_lk[tid] = lk;
-        }
-        if ((a.mask & YVMOE_HEAD_EO) && tid < D) {
-            const float hv = hsum(4 * E + tid);
-            s_h[tid] = hv / (1.f + expf(-hv));  // SiLU
+            s_ph[q][o] = h;
         }
         __syncthreads();
-        // ---------------------------------------------------------------- Expert-Oriented
-        // silu(input_encoder.0 x) · M with M = input_encoder.2ᵀ · encoded_expertsᵀ [D][E]
-        float eo = 0.f;
-        if (a.mask & YVMOE_HEAD_EO) {
-            float sum = 0.f;
-            if (o < E) {
-                for (int d0 = q; d0 < D; d0 += 16 * Q) {  // 16 loads in flight per thread
-                    float mv[16];
+        float hicl = 0.f, eo = 0.f;
+        if (is_e) {
+            if (hicl_on) {
+                hicl = s_ph[0][tid];
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int d = d0 + Q * i;
-                        mv[i] = d < D ? a.eo_mat[d * E + o] : 0.f;
-                    }
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int d = d0 + Q * i;
-                        if (d < D) sum += s_h[d] * mv[i];
-                    }
-                }
+                for (int i = 1; i < Q; ++i) hicl += s_ph[i][tid];
             }
-            s_part[q][o] = sum;
-            __syncthreads();
-            if (is_e) eo = ((s_part[0][tid] + s_part[1][tid]) + s_part[2][tid]) + s_part[3][tid];
+            if (eo_on) {
+                eo = s_pe[0][tid];
+#pragma unroll
+                for (int i = 1; i < Q; ++i) eo += s_pe[i][tid];
+            }
         }
         // ---------------------------------------------------------------- SoftMoE, logits, loss
         auto logit = [&](float soft) {
             float l = gate;
-            if (a.mask & YVMOE_HEAD_HICL) l = l + a.w_hicl * hicl;
+            if (hicl_on) l = l + a.w_hicl * hicl;
             if (a.mask & YVMOE_HEAD_GOT) l = l + a.w_got * got;
             if (a.mask & YVMOE_HEAD_SOFT) l = l + a.w_soft * soft;
-            if (a.mask & YVMOE_HEAD_EO) l = l + a.w_eo * eo;
-            if (a.modal_id != nullptr) {
-                const int md = a.modal_id[t];
-                if (md >= 0 && md < a.nmod) l = l + a.modal[tid * a.nmod + md];
-            }
-            if (a.ebias != nullptr) l = l + a.ebias[tid];
+            if (eo_on) l = l + a.w_eo * eo;
+            if (a.modal_id != nullptr) l = l + modal_e;
+            if (a.ebias != nullptr) l = l + bias_e;
             l = l / a.temp;
-            a.logits[(long long)t * E + tid] = l;
+            a.logits[(long long)t * E + tt] = l;
             return l;
         };
         if (E <= 64) {
@@ -549,40 +592,41 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
 
 // loss = alpha · Σ_e (mean_n score - 1/E)² + capacity term + z_alpha · mean(logits²)
 //        + 0.01 · (mean_n Σ_e soft - budget)²   (gate.py:433-444, :556-610)
-// 16 waves; wave w sums columns w, w + 16, ... (each lane a fixed stride of groups, then the
-// lanes by butterfly), all of its columns' loads in flight together.
-constexpr int kLossCols = (YVMOE_MAX_EXPERTS + 2 + 15) / 16;
+// Thread c sums column c of the per-work-group sums in group order (16 loads in flight), then
+// the load-balance sum over experts is one wave reduction per wave and the waves in order.
 __global__ __launch_bounds__(1024) void moegate_loss_kernel(const float* __restrict__ part, int G,
                                                             int E, int N, float lb_alpha,
                                                             float z_alpha, float budget,
                                                             float cap_loss, int has_soft,
                                                             float* __restrict__ loss) {
     __shared__ float col[YVMOE_MAX_EXPERTS + 2];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    float s[kLossCols];
+    __shared__ float red[16];
+    const int c = threadIdx.x, lane = c & 63, wave = c >> 6;
+    if (c < E + 2) {
+        const float* pc = part + (long long)c * G;
+        float sum = 0.f;
+        for (int g0 = 0; g0 < G; g0 += 16) {
+            float v[16];
 #pragma unroll
-    for (int i = 0; i < kLossCols; ++i) s[i] = 0.f;
-    for (int g = lane; g < G; g += 64) {
+            for (int i = 0; i < 16; ++i) v[i] = g0 + i < G ? pc[g0 + i] : 0.f;
 #pragma unroll
-        for (int i = 0; i < kLossCols; ++i) {
-            const int c = wave + 16 * i;
-            if (c < E + 2) s[i] += part[(long long)c * G + g];
+            for (int i = 0; i < 16; ++i) sum += v[i];
         }
-    }
-#pragma unroll
-    for (int i = 0; i < kLossCols; ++i) {
-        const int c = wave + 16 * i;
-        const float v = wave_sum(s[i]);
-        if (lane == 0 && c < E + 2) col[c] = v;
+        col[c] = sum;
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        const float fn = (float)N;
-        float lb = 0.f;
-        for (int e = 0; e < E; ++e) {
-            const float d = col[e] / fn - 1.f / (float)E;
-            lb += d * d;
-        }
+    const float fn = (float)N;
+    float d = 0.f;
+    if (c < E) {
+        d = col[c] / fn - 1.f / (float)E;
+        d = d * d;
+    }
+    d = wave_sum(d);
+    if (lane == 0) red[wave] = d;
+    __syncthreads();
+    if (c == 0) {
+        float lb = red[0];
+        for (int w = 1; w < 16; ++w) lb += red[w];
         float total = lb_alpha * lb + cap_loss + z_alpha * (col[E] / ((float)N * (float)E));
         if (has_soft) {
             const float ac = col[E + 1] / fn - budget;
@@ -621,7 +665,9 @@ int moegate_launch(const void* x, int act, int N, const yvmoe_moegate* g, const 
     float* proj = (float*)(ws + w.proj);
     float* part = (float*)(ws + w.loss);
     if (N > 0) {
-        int rc = dense_partials_launch(x, act, N, H, g->w_proj, P, proj, P, st, "moegate_proj");
+        const bool hicl = (g->heads & YVMOE_HEAD_HICL) != 0;
+        int rc = dense_partials_launch(x, act, N, H, g->w_proj, P, proj, P, hicl ? g->dg_bias : nullptr,
+                                       hicl ? g->dg_dim : 0, st, "moegate_proj");
         if (rc) return rc;
         GateArgs a{};
         a.heads = proj + hoff;
@@ -651,12 +697,28 @@ int moegate_launch(const void* x, int act, int N, const yvmoe_moegate* g, const 
         a.mask = g->heads;
         a.logits = logits;
         a.part = part;
-        a.nv = ceil_div(g->dg_dim, kGateNT);
-        switch (a.nsplit) {
-            case 1: moegate_token_kernel<kGateNT, 1><<<w.groups, kGateNT, 0, st>>>(a); break;
-            case 2: moegate_token_kernel<kGateNT, 2><<<w.groups, kGateNT, 0, st>>>(a); break;
-            default: set_error("moegate: %d partial sums of the projection", a.nsplit); return YVMOE_ERR_SHAPE;
+        // 1024 threads: measured faster than two 512-thread work-groups per CU (decode and
+        // prefill)
+        // 16-byte row loads per thread: 1, 2, 4 or 8 (DG width up to 4K, 8K, 16K, 32K)
+        const int j4 = (g->heads & YVMOE_HEAD_HICL) == 0 ? 1 : g->dg_dim <= 4096 ? 1 : g->dg_dim <= 8192 ? 2
+                       : g->dg_dim <= 16384 ? 4 : 8;
+        a.nv = 4 * j4;
+        if (a.nsplit != 1 && a.nsplit != 2) {
+            set_error("moegate: %d partial sums of the projection", a.nsplit);
+            return YVMOE_ERR_SHAPE;
         }
+#define YV_TOK(NS, J4) moegate_token_kernel<1024, NS, J4><<<w.groups, 1024, 0, st>>>(a)
+        switch (j4 * 10 + a.nsplit) {
+            case 11: YV_TOK(1, 1); break;
+            case 12: YV_TOK(2, 1); break;
+            case 21: YV_TOK(1, 2); break;
+            case 22: YV_TOK(2, 2); break;
+            case 41: YV_TOK(1, 4); break;
+            case 42: YV_TOK(2, 4); break;
+            case 81: YV_TOK(1, 8); break;
+            default: YV_TOK(2, 8); break;
+        }
+#undef YV_TOK
         YV_LAUNCH_CHECK("moegate_token");
     }
     moegate_loss_kernel<<<1, 1024, 0, st>>>(part, w.groups, E, N, g->load_balance_alpha,

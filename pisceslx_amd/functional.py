@@ -273,3 +273,38 @@ def moegate_logits(x2d: torch.Tensor, gate: MoEGateState, modal_id: Optional[tor
                                                 workspace.numel(), _stream(dev)),
                "yvmoe_moegate_logits")
     return logits, loss
+
+
+def moegate_forward(x2d: torch.Tensor, gate: MoEGateState, top_k: int,
+                    modal_id: Optional[torch.Tensor] = None,
+                    workspace: Optional[torch.Tensor] = None):
+    """YvMoEGate logits [N, E], loss [1] and the fixed-mode routing, in one library call.
+
+    Returns (logits, loss, Routing, workspace); the workspace's routing region is what
+    expert_ffn reads, so it can be passed on to expert_ffn with the routing.
+    """
+    dev = _require_cuda(x2d, modal_id, *gate.tensors())
+    act = _act(x2d.dtype)
+    N, H = x2d.shape
+    if H != gate.hidden:
+        raise ValueError(f"hidden size {H} does not match the gate ({gate.hidden})")
+    if modal_id is not None and (modal_id.dtype != torch.int32 or modal_id.numel() != N):
+        raise ValueError("modal_id must be int32 [N]")
+    E = gate.num_experts
+    g = gate.struct()
+    need = int(_lib.lib().yvmoe_moegate_forward_workspace_bytes(N, act, top_k, ctypes.byref(g)))
+    if need == 0:
+        raise ValueError("yvmoe_moegate_forward_workspace_bytes rejected the gate state / top_k")
+    if workspace is None or workspace.numel() < need:
+        workspace = _workspace(need, dev)
+    logits = torch.empty(N, E, dtype=torch.float32, device=dev)
+    loss = torch.empty(1, dtype=torch.float32, device=dev)
+    routing = Routing.empty(N, E, top_k, dev)
+    o = routing.struct()
+    _lib.check(_lib.lib().yvmoe_moegate_forward(x2d.data_ptr() if N > 0 else None, act, N,
+                                                 ctypes.byref(g), _ptr(modal_id), top_k,
+                                                 logits.data_ptr() if N > 0 else None,
+                                                 loss.data_ptr(), ctypes.byref(o),
+                                                 workspace.data_ptr(), workspace.numel(),
+                                                 _stream(dev)), "yvmoe_moegate_forward")
+    return logits, loss, routing, workspace

@@ -265,6 +265,9 @@ class YvMoEGate(nn.Module):
         self._state_key = None
         self._register_load_state_dict_pre_hook(self._skip_unbuilt_keys)
         self.last_routing: Optional[yvf.Routing] = None
+        self._workspace: Optional[torch.Tensor] = None
+        self._tlist_key = None
+        self._tlist_probe = ()
 
     def _skip_unbuilt_keys(self, state_dict, prefix, *args):
         for k in [k for k in state_dict if k.startswith(tuple(prefix + p for p in self._SKIPPED_PREFIXES))]:
@@ -289,7 +292,7 @@ class YvMoEGate(nn.Module):
     def gate_state(self, act: int, seq_len: int) -> yvf.MoEGateState:
         """Regrouped device tensors for yvmoe_moegate_logits (rebuilt when a parameter,
         buffer or the pruned set changes)."""
-        tensors = list(self.parameters()) + list(self.buffers())
+        tensors = self._tensor_list()
         key = (act, seq_len >= 8192, tuple(sorted(self._pruned_heads)),
                tuple((t.data_ptr(), t._version) for t in tensors))
         if self._state is not None and self._state_key == key:
@@ -340,6 +343,17 @@ class YvMoEGate(nn.Module):
         self._state_key = key
         return self._state
 
+    def _tensor_list(self):
+        """Parameters and buffers, listed once per module structure (pruning or device moves
+        change the objects, which changes the key)."""
+        ids = (len(self._parameters), len(self._buffers), tuple(sorted(self._pruned_heads)))
+        if getattr(self, "_tlist_key", None) != ids or any(
+                t is not p for t, p in zip(self._tlist_probe, (self.gate.weight, self.temperature))):
+            self._tlist = list(self.parameters()) + list(self.buffers())
+            self._tlist_probe = (self.gate.weight, self.temperature)
+            self._tlist_key = ids
+        return self._tlist
+
     def fixed_router_state(self) -> yvf.RouterState:
         """The fixed-mode routing (softmax, top-k, softmax of the k scores) on the gate logits."""
         return yvf.RouterState(self.num_experts, self.hidden_size, min(self.top_k, self.num_experts),
@@ -364,7 +378,6 @@ class YvMoEGate(nn.Module):
         act = yvf._act(x2d.dtype)
         st = self.gate_state(act, S)
         mid = None if modal_id is None else self._modal_ids(modal_id, B, S, x.device)
-        logits, loss = yvf.moegate_logits(x2d, st, mid)
         N = x2d.shape[0]
         # PathMoE (gate.py:418-431): one routing shared by a stage of calls with the same token
         # count; later calls of a stage keep it (their own logits still set the loss)
@@ -376,10 +389,15 @@ class YvMoEGate(nn.Module):
                 self._path_moe_cache = None
                 self._path_moe_signature = sig
             reuse = self._path_moe_layer_idx != 0 and self._path_moe_cache is not None
+        ws = self._workspace if getattr(self, "_workspace", None) is not None and \
+            self._workspace.device == x.device else None
+        logits, loss, fresh, ws = yvf.moegate_forward(x2d, st, min(self.top_k, self.num_experts),
+                                                      mid, workspace=ws)
+        self._workspace = ws
         if reuse:
             routing = self._path_moe_cache
         else:
-            routing = yvf.route(logits, self.fixed_router_state(), predictor=False)
+            routing = fresh
             if self._path_moe_stage_size > 1:
                 self._path_moe_cache = routing
         if self._path_moe_stage_size > 1:
