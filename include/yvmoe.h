@@ -27,6 +27,9 @@
  *   yvmoe_moegate_logits -> YvMoEGate.forward in eval mode up to the top-k (steps 2-8 and the
  *                           loss of step 13), model/moe/gate.py:310-393, :433-444; the top-k
  *                           and its softmax (gate.py:414-416) are yvmoe_route in fixed mode
+ *   yvmoe_moegate_forward-> YvMoEGate.forward in eval mode (logits, loss and routing)
+ *   yvmoe_forward_moegate-> YvDynamicMoELayer.forward with its YvMoEGate router
+ *                           model/moe/layer.py:867-963 (inference)
  */
 #ifndef YVMOE_H
 #define YVMOE_H
@@ -277,6 +280,23 @@ size_t yvmoe_moegate_forward_workspace_bytes(int32_t n_tokens, int32_t act_dtype
 int32_t yvmoe_moegate_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
                               const yvmoe_moegate* gate, const int32_t* modal_id, int32_t top_k,
                               float* logits, float* loss, yvmoe_routing* routing,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The whole layer with YvMoEGate as its router, as YvDynamicMoELayer builds it
+ * (model/moe/layer.py:754-777, :867-963): yvmoe_moegate_forward, then yvmoe_expert_ffn and
+ * yvmoe_combine on that routing. route_logits: NULL to route on this call's logits, or the
+ * logits [N][E] of an earlier call to route on instead (the PathMoE stage cache,
+ * gate.py:418-431; the loss still comes from this call's logits).
+ */
+size_t yvmoe_forward_moegate_workspace_bytes(int32_t n_tokens, int32_t act_dtype, int32_t top_k,
+                                             const yvmoe_moegate* gate,
+                                             const yvmoe_expert_weights* experts);
+int32_t yvmoe_forward_moegate(const void* x, int32_t act_dtype, int32_t n_tokens,
+                              const yvmoe_moegate* gate, const int32_t* modal_id, int32_t top_k,
+                              const float* route_logits, const yvmoe_expert_weights* experts,
+                              const float* mix, const void* skip, void* out, void* shared_out,
+                              yvmoe_routing* routing, float* logits, float* loss,
                               void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus

@@ -50,6 +50,8 @@ EXPORTED_SYMBOLS = (
     "yvmoe_moegate_logits",
     "yvmoe_moegate_forward_workspace_bytes",
     "yvmoe_moegate_forward",
+    "yvmoe_forward_moegate_workspace_bytes",
+    "yvmoe_forward_moegate",
 )
 
 # YvMoEGate auxiliary heads (YVMOE_HEAD_*)
@@ -168,6 +170,13 @@ def _declare(l: ctypes.CDLL) -> None:
     l.yvmoe_moegate_forward.restype = i32
     l.yvmoe_moegate_forward.argtypes = [vp, i32, i32, ctypes.POINTER(MoEGate), vp, i32, vp, vp,
                                         ctypes.POINTER(Routing), vp, sz, vp]
+    l.yvmoe_forward_moegate_workspace_bytes.restype = sz
+    l.yvmoe_forward_moegate_workspace_bytes.argtypes = [i32, i32, i32, ctypes.POINTER(MoEGate),
+                                                        ctypes.POINTER(ExpertWeights)]
+    l.yvmoe_forward_moegate.restype = i32
+    l.yvmoe_forward_moegate.argtypes = [vp, i32, i32, ctypes.POINTER(MoEGate), vp, i32, vp,
+                                        ctypes.POINTER(ExpertWeights), vp, vp, vp, vp,
+                                        ctypes.POINTER(Routing), vp, vp, vp, sz, vp]
     l.yvmoe_forward.restype = i32
     l.yvmoe_forward.argtypes = [vp, i32, i32, ctypes.POINTER(Router), ctypes.POINTER(ExpertWeights),
                                 vp, vp, vp, vp, ctypes.POINTER(Routing), vp, sz, vp]

@@ -349,4 +349,82 @@ int32_t yvmoe_moegate_forward(const void* x, int32_t act_dtype, int32_t n_tokens
     return route_launch(n_tokens > 0 ? logits : nullptr, E, nullptr, E, n_tokens, &r, -1, routing, ws, st);
 }
 
+static size_t forward_moegate_bytes(int N, int act, int k, const yvmoe_moegate* g,
+                                    const yvmoe_expert_weights* w) {
+    const size_t a = gate_ws(N, act, g).bytes;
+    const size_t b = ffn_ws(N, k, w->num_routed, w->num_shared, w->ffn, act).bytes +
+                     y_bytes(N, k, w->num_shared, w->hidden, act);
+    return route_ws(N, g->num_experts, k).bytes + (a > b ? a : b);
+}
+
+size_t yvmoe_forward_moegate_workspace_bytes(int32_t n_tokens, int32_t act_dtype, int32_t top_k,
+                                             const yvmoe_moegate* gate,
+                                             const yvmoe_expert_weights* experts) {
+    if (n_tokens < 0 || check_moegate(gate, act_dtype) != YVMOE_OK || experts == nullptr) return 0;
+    if (top_k < 1 || top_k > YVMOE_MAX_TOPK || top_k > gate->num_experts) return 0;
+    return forward_moegate_bytes(n_tokens, act_dtype, top_k, gate, experts);
+}
+
+int32_t yvmoe_forward_moegate(const void* x, int32_t act_dtype, int32_t n_tokens,
+                              const yvmoe_moegate* gate, const int32_t* modal_id, int32_t top_k,
+                              const float* route_logits, const yvmoe_expert_weights* experts,
+                              const float* mix, const void* skip, void* out, void* shared_out,
+                              yvmoe_routing* routing, float* logits, float* loss,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = check_moegate(gate, act_dtype);
+    if (rc) return rc;
+    rc = check_experts(experts, act_dtype);
+    if (rc) return rc;
+    rc = check_routing(routing, n_tokens);
+    if (rc) return rc;
+    const int E = gate->num_experts, k = top_k, S = experts->num_shared;
+    YV_REQUIRE(E == experts->num_routed && gate->hidden == experts->hidden, YVMOE_ERR_SHAPE,
+               "gate (E=%d, H=%d) and experts (E=%d, H=%d) disagree", E, gate->hidden,
+               experts->num_routed, experts->hidden);
+    YV_REQUIRE(k >= 1 && k <= YVMOE_MAX_TOPK && k <= E, YVMOE_ERR_SHAPE,
+               "top_k=%d outside [1, min(E=%d, %d)]", k, E, YVMOE_MAX_TOPK);
+    YV_REQUIRE(n_tokens >= 0, YVMOE_ERR_ARG, "n_tokens=%d < 0", n_tokens);
+    YV_REQUIRE(loss != nullptr, YVMOE_ERR_ARG, "loss is NULL");
+    YV_REQUIRE(n_tokens == 0 || (x && out && logits), YVMOE_ERR_ARG, "NULL pointer");
+    YV_REQUIRE(S == 0 || mix != nullptr, YVMOE_ERR_ARG, "shared experts need mix weights");
+    YV_REQUIRE(modal_id == nullptr || (gate->modal_affinity && gate->n_modalities > 0),
+               YVMOE_ERR_ARG, "modal_id needs modal_affinity");
+    const long long rows = (long long)n_tokens * (k + S);
+    YV_REQUIRE(rows * experts->hidden < (1ll << 40) && (long long)n_tokens * k < (1ll << 31),
+               YVMOE_ERR_SHAPE, "problem too large");
+    const size_t need = forward_moegate_bytes(n_tokens, act_dtype, k, gate, experts);
+    YV_REQUIRE(workspace != nullptr && workspace_bytes >= need, YVMOE_ERR_WORKSPACE,
+               "workspace %zu bytes, need %zu", workspace_bytes, need);
+    hipStream_t st = (hipStream_t)stream;
+    char* ws = (char*)workspace;
+    const int N = n_tokens;
+    const size_t rbytes = route_ws(N, E, k).bytes;
+    // the gate's region is reused by the expert FFN once the routing has been computed
+    rc = moegate_launch(x, act_dtype, N, gate, modal_id, logits, loss, ws + rbytes, st);
+    if (rc) return rc;
+    yvmoe_router r{};
+    r.num_experts = E;
+    r.hidden = gate->hidden;
+    r.top_k = k;
+    r.fixed_shape_mode = 1;
+    const bool small = N > 0 && N <= kSmallRouteTok;
+    TileTable tiles{};
+    if (small)
+        tiles = ffn_tile_table(N, k, E, S, experts->ffn, act_dtype,
+                               ffn_tile_rows(act_dtype, N, k, E, experts->hidden, experts->ffn,
+                                             experts->format),
+                               ws);
+    const float* lsrc = route_logits != nullptr ? route_logits : logits;
+    rc = route_launch(N > 0 ? lsrc : nullptr, E, nullptr, E, N, &r, -1, routing, ws, st, 1, 0,
+                      small ? &tiles : nullptr);
+    if (rc) return rc;
+    if (N == 0) return YVMOE_OK;
+    void* y = ws + rbytes + ffn_ws(N, k, E, S, experts->ffn, act_dtype).bytes;
+    rc = expert_ffn_launch(x, act_dtype, N, k, experts, routing, y, ws, st, small);
+    if (rc) return rc;
+    return combine_launch(y, act_dtype, N, experts->hidden, k, S, routing, mix, skip, out,
+                          shared_out, st);
+}
+
 }  // extern "C"

@@ -308,3 +308,48 @@ def moegate_forward(x2d: torch.Tensor, gate: MoEGateState, top_k: int,
                                                  workspace.data_ptr(), workspace.numel(),
                                                  _stream(dev)), "yvmoe_moegate_forward")
     return logits, loss, routing, workspace
+
+
+def moe_forward_moegate(x2d: torch.Tensor, gate: MoEGateState, top_k: int, experts: PackedExperts,
+                        mix: Optional[torch.Tensor], skip: Optional[torch.Tensor],
+                        modal_id: Optional[torch.Tensor] = None,
+                        route_logits: Optional[torch.Tensor] = None,
+                        workspace: Optional[torch.Tensor] = None):
+    """Whole layer with a YvMoEGate router. Returns (out, shared_out or None, Routing, logits,
+    loss, workspace); ``route_logits`` (fp32 [N, E]) routes on earlier logits instead."""
+    dev = _require_cuda(x2d, mix, skip, modal_id, route_logits, *gate.tensors(), *experts.tensors())
+    act = _act(x2d.dtype)
+    N, H = x2d.shape
+    if H != experts.hidden or H != gate.hidden:
+        raise ValueError(f"hidden size {H} does not match the layer ({experts.hidden})")
+    if skip is not None and (skip.shape != x2d.shape or skip.dtype != x2d.dtype):
+        raise ValueError("skip buffer must match x")
+    if mix is not None and (mix.dtype != torch.float32 or mix.numel() != experts.num_shared):
+        raise ValueError("mix must be fp32 [S]")
+    if modal_id is not None and (modal_id.dtype != torch.int32 or modal_id.numel() != N):
+        raise ValueError("modal_id must be int32 [N]")
+    E, S = gate.num_experts, experts.num_shared
+    if route_logits is not None and (route_logits.dtype != torch.float32 or
+                                     tuple(route_logits.shape) != (N, E)):
+        raise ValueError("route_logits must be fp32 [N, E]")
+    g = gate.struct()
+    e = experts.struct()
+    need = int(_lib.lib().yvmoe_forward_moegate_workspace_bytes(N, act, top_k, ctypes.byref(g),
+                                                                ctypes.byref(e)))
+    if need == 0:
+        raise ValueError("yvmoe_forward_moegate_workspace_bytes rejected the gate / experts / top_k")
+    if workspace is None or workspace.numel() < need:
+        workspace = _workspace(need, dev)
+    routing = Routing.empty(N, E, top_k, dev)
+    out = torch.empty_like(x2d)
+    shared_out = torch.empty_like(x2d) if S > 0 else None
+    logits = torch.empty(N, E, dtype=torch.float32, device=dev)
+    loss = torch.empty(1, dtype=torch.float32, device=dev)
+    o = routing.struct()
+    _lib.check(_lib.lib().yvmoe_forward_moegate(
+        x2d.data_ptr() if N > 0 else None, act, N, ctypes.byref(g), _ptr(modal_id), top_k,
+        _ptr(route_logits), ctypes.byref(e), _ptr(mix), _ptr(skip),
+        out.data_ptr() if N > 0 else None, _ptr(shared_out) if N > 0 else None, ctypes.byref(o),
+        logits.data_ptr() if N > 0 else None, loss.data_ptr(), workspace.data_ptr(),
+        workspace.numel(), _stream(dev)), "yvmoe_forward_moegate")
+    return out, shared_out, routing, logits, loss, workspace

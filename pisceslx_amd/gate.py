@@ -379,33 +379,41 @@ class YvMoEGate(nn.Module):
         st = self.gate_state(act, S)
         mid = None if modal_id is None else self._modal_ids(modal_id, B, S, x.device)
         N = x2d.shape[0]
-        # PathMoE (gate.py:418-431): one routing shared by a stage of calls with the same token
-        # count; later calls of a stage keep it (their own logits still set the loss)
-        reuse = False
-        if self._path_moe_stage_size > 1:
-            sig = (N, self.training)
-            if sig != self._path_moe_signature:
-                self._path_moe_layer_idx = 0
-                self._path_moe_cache = None
-                self._path_moe_signature = sig
-            reuse = self._path_moe_layer_idx != 0 and self._path_moe_cache is not None
+        cached = self.path_moe_begin(N)
         ws = self._workspace if getattr(self, "_workspace", None) is not None and \
             self._workspace.device == x.device else None
         logits, loss, fresh, ws = yvf.moegate_forward(x2d, st, min(self.top_k, self.num_experts),
                                                       mid, workspace=ws)
         self._workspace = ws
-        if reuse:
-            routing = self._path_moe_cache
-        else:
-            routing = fresh
-            if self._path_moe_stage_size > 1:
-                self._path_moe_cache = routing
-        if self._path_moe_stage_size > 1:
-            self._path_moe_layer_idx = (self._path_moe_layer_idx + 1) % self._path_moe_stage_size
+        routing = cached[1] if cached is not None else fresh
+        self.path_moe_end(None if cached is not None else (logits, fresh))
         self.last_routing = routing
         self.last_logits = logits
         self._last_loss_f32 = loss
         return routing.weights.to(x.dtype), routing.indices, loss.reshape(()).to(x.dtype)
+
+    # PathMoE (gate.py:418-431): one routing shared by a stage of calls with the same token
+    # count; the later calls of a stage keep it (their own logits still set the loss).
+    def path_moe_begin(self, n_tokens: int):
+        """Stage bookkeeping before a forward: the cached (logits, routing) to reuse, or None."""
+        if self._path_moe_stage_size <= 1:
+            return None
+        sig = (n_tokens, self.training)
+        if sig != self._path_moe_signature:
+            self._path_moe_layer_idx = 0
+            self._path_moe_cache = None
+            self._path_moe_signature = sig
+        if self._path_moe_layer_idx != 0 and self._path_moe_cache is not None:
+            return self._path_moe_cache
+        return None
+
+    def path_moe_end(self, fresh) -> None:
+        """After a forward: cache this call's (logits, routing) when it routed afresh."""
+        if self._path_moe_stage_size <= 1:
+            return
+        if fresh is not None:
+            self._path_moe_cache = fresh
+        self._path_moe_layer_idx = (self._path_moe_layer_idx + 1) % self._path_moe_stage_size
 
     def prune_routing_heads(self, prune_threshold: float = 0.05) -> None:
         """Drop auxiliary heads whose sparse gate sigmoid is below the threshold (gate.py:466-489)."""

@@ -1,12 +1,14 @@
 """Yv MoE layer forward for MI355X — drop-in for YvDynamicMoELayer / YvDeepSeekMoELayer.
 
 Reference: model/moe/layer.py:519-963 (YvDynamicMoELayer) and :967-1396
-(YvDeepSeekMoELayer), with the router swapped for YvStableMoEGate as the inference path
-names (the reference's own YvMoELayer builds that gate, model/moe/gate.py:1498-1510).
+(YvDeepSeekMoELayer). The router is what the reference's ``_build_router`` builds, YvMoEGate
+(layer.py:754-777), by default (``router="moegate"``); ``router="stable"`` swaps in
+YvStableMoEGate, the gate the reference's YvMoELayer builds (model/moe/gate.py:1498-1510).
 
 ``forward(x, subconscious_hints=None, modal_id=None) -> (out, loss)`` keeps the reference
-signature; ``subconscious_hints`` and ``modal_id`` are accepted and ignored, exactly as the
-reference does for this gate (layer.py:903-909). The stateful UltraMem skip residual
+signature; ``subconscious_hints`` is accepted and ignored, ``modal_id`` goes to YvMoEGate
+(layer.py:903-909; YvStableMoEGate takes none). The loss is YvMoEGate's routing loss (0 with
+YvStableMoEGate, whose inference forward has none). The stateful UltraMem skip residual
 (layer.py:739-753) is kept: when shared experts exist, 0.1 * the previous call's shared
 output is added if the shapes agree, and the buffer is replaced by this call's shared output.
 
@@ -27,7 +29,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from . import functional as yvf
-from .gate import YvStableMoEGate
+from .gate import YvMoEGate, YvStableMoEGate
 from .quant import ExpertPacker, FORMAT_BY_NAME, PackedExperts
 
 
@@ -44,7 +46,8 @@ class YvDynamicMoELayer(nn.Module):
 
     def __init__(self, cfg: Any, device=None, dtype=None, num_shared_experts: int = 1,
                  use_fine_grained: bool = False, num_sub_experts: int = 1,
-                 compute_mode: str = "default", weight_format: Optional[str] = None):
+                 compute_mode: str = "default", weight_format: Optional[str] = None,
+                 router: Optional[str] = None):
         super().__init__()
         if compute_mode != "default":
             raise NotImplementedError("compute_split experts (layer.py:646-676) are not supported")
@@ -65,15 +68,28 @@ class YvDynamicMoELayer(nn.Module):
             weight_format = "bf16" if self.dtype == torch.bfloat16 else "f32"
         self.weight_format = FORMAT_BY_NAME[weight_format]
         H = self.hidden_size
-        self.router = YvStableMoEGate(
-            H, self.num_experts, top_k=self.top_k, device=device, dtype=dtype,
-            capacity_factor=getattr(cfg, "moe_capacity_factor", 1.0),
-            min_capacity=getattr(cfg, "moe_min_capacity", 4),
-            prediction_horizon=getattr(cfg, "moe_prediction_horizon", 10),
-            fixed_shape_mode=getattr(cfg, "moe_fixed_shape_mode", H <= 768),
-            enable_dynamic_capacity=getattr(cfg, "enable_dynamic_capacity", True),
-            enable_cognitive_density=getattr(cfg, "enable_cognitive_density", False))
+        if router is None:
+            router = getattr(cfg, "moe_router", "moegate")
+        if router == "moegate":
+            self.router = YvMoEGate(
+                H, self.num_experts, top_k=self.top_k, device=device, dtype=dtype,
+                load_balance_alpha=getattr(cfg, "moe_load_balance_alpha", 0.01),
+                noise_std=getattr(cfg, "moe_noise_std", 0.1),
+                enable_cognitive_density=getattr(cfg, "enable_cognitive_density", False), cfg=cfg)
+        elif router == "stable":
+            self.router = YvStableMoEGate(
+                H, self.num_experts, top_k=self.top_k, device=device, dtype=dtype,
+                capacity_factor=getattr(cfg, "moe_capacity_factor", 1.0),
+                min_capacity=getattr(cfg, "moe_min_capacity", 4),
+                prediction_horizon=getattr(cfg, "moe_prediction_horizon", 10),
+                fixed_shape_mode=getattr(cfg, "moe_fixed_shape_mode", H <= 768),
+                enable_dynamic_capacity=getattr(cfg, "enable_dynamic_capacity", True),
+                enable_cognitive_density=getattr(cfg, "enable_cognitive_density", False))
+        else:
+            raise ValueError(f"router={router!r}: 'moegate' or 'stable'")
+        self._router_kind = router
         self._router_mode = "token_gate"
+        self._workspace: Optional[torch.Tensor] = None
         S = num_shared_experts
         self.experts_packed = self._random_experts(device)
         if S > 0:
@@ -154,18 +170,36 @@ class YvDynamicMoELayer(nn.Module):
         if not x2d.is_contiguous():
             x2d = x2d.contiguous()
         act = yvf._act(x2d.dtype)
-        st = self.router.router_state(act)
         has_shared = self.num_shared_experts > 0
         skip = None
         if has_shared:
             buf = self._apply_skip_residual_buffer((B, Sq, H))
             skip = None if buf is None else buf.reshape(-1, H)
-        out, shared_out, routing = yvf.moe_forward(x2d, st, self.experts_packed, self._mix(), skip)
+        ws = self._workspace if self._workspace is not None and self._workspace.device == x.device else None
+        if self._router_kind == "moegate":
+            g = self.router
+            st = g.gate_state(act, Sq)
+            mid = None if modal_id is None else g._modal_ids(modal_id, B, Sq, x.device)
+            cached = g.path_moe_begin(x2d.shape[0])
+            out, shared_out, routing, logits, loss, ws = yvf.moe_forward_moegate(
+                x2d, st, min(self.top_k, self.num_experts), self.experts_packed, self._mix(), skip,
+                modal_id=mid, route_logits=None if cached is None else cached[0], workspace=ws)
+            g.path_moe_end(None if cached is not None else (logits, routing))
+            g.last_routing, g.last_logits, g._last_loss_f32 = routing, logits, loss
+            loss = loss.reshape(()).to(x.dtype)
+        else:
+            st = self.router.router_state(act)
+            if ws is None or ws.numel() < yvf.workspace_bytes(x2d.shape[0], act, st, self.experts_packed):
+                ws = None
+            out, shared_out, routing = yvf.moe_forward(x2d, st, self.experts_packed, self._mix(), skip,
+                                                       workspace=ws)
+            loss = torch.tensor(0.0, device=x.device, dtype=x.dtype)
+        self._workspace = ws
         if has_shared:
             self._skip_buffer = shared_out.view(B, Sq, H)
         self.last_routing = routing
         self._step += 1
-        return out.view(B, Sq, H), torch.tensor(0.0, device=x.device, dtype=x.dtype)
+        return out.view(B, Sq, H), loss
 
 
 class YvDeepSeekMoELayer(YvDynamicMoELayer):
@@ -176,11 +210,12 @@ class YvDeepSeekMoELayer(YvDynamicMoELayer):
     loaded state_dict replaces, so it is not reproduced.
     """
 
-    def __init__(self, cfg: Any, device=None, dtype=None, weight_format: Optional[str] = None):
+    def __init__(self, cfg: Any, device=None, dtype=None, weight_format: Optional[str] = None,
+                 router: Optional[str] = None):
         super().__init__(cfg, device=device, dtype=dtype,
                          num_shared_experts=getattr(cfg, "moe_shared_experts", 1),
                          use_fine_grained=getattr(cfg, "moe_fine_grained", True),
                          num_sub_experts=getattr(cfg, "moe_num_sub_experts", 4),
                          compute_mode=getattr(cfg, "moe_compute_mode", "default"),
-                         weight_format=weight_format)
+                         weight_format=weight_format, router=router)
         self.diversity_weight = getattr(cfg, "diversity_weight", 0.01)

@@ -1,6 +1,8 @@
 """The drop-in modules on the GPU: YvDeepSeekMoELayer loaded from a reference-style state
-dict, called the way YvHybridBlock calls it, against the CPU oracle; the stateful skip
-residual across calls (model/moe/layer.py:741-753, mirrored from
+dict, called the way YvHybridBlock calls it, against the CPU oracle — with the YvStableMoEGate
+router and with the YvMoEGate router the reference's layers build (model/moe/layer.py:754-777),
+including modal ids, the routing loss and the PathMoE stage cache; the stateful skip residual
+across calls (model/moe/layer.py:741-753, mirrored from
 tools/test/test_moe_routing_contract.py:187-201); the YvStableMoEGate contract
 (tools/test/test_moe_routing_contract.py:65-81)."""
 import numpy as np
@@ -8,8 +10,10 @@ import pytest
 import torch
 
 from oracle import moe_oracle
+from oracle import moegate_oracle as mg
 from pisceslx_amd import YvDeepSeekMoELayer, YvStableMoEGate
 from pisceslx_amd import functional as yvf
+from pisceslx_amd.gate import YvMoEGate
 
 from helpers import cosine
 
@@ -76,7 +80,8 @@ def _oracle_call(layer, x, skip):
 @pytest.mark.parametrize("fmt", ["int8", "bf16"])
 def test_deepseek_layer_drop_in(cuda, oracle, fmt):
     cfg = Cfg()
-    layer = YvDeepSeekMoELayer(cfg, device=cuda, dtype=torch.bfloat16, weight_format=fmt).eval()
+    layer = YvDeepSeekMoELayer(cfg, device=cuda, dtype=torch.bfloat16, weight_format=fmt,
+                               router="stable").eval()
     layer.load_reference_state_dict(reference_state_dict(cfg))
     g = torch.Generator(device=cuda).manual_seed(1)
     x1 = torch.randn(2, 17, cfg.hidden_size, device=cuda, generator=g).to(torch.bfloat16)
@@ -128,3 +133,104 @@ def test_layer_rejects_training_mode(cuda):
     layer = YvDeepSeekMoELayer(Cfg(), device=cuda, dtype=torch.bfloat16, weight_format="bf16")
     with pytest.raises(NotImplementedError):
         layer.train()(torch.randn(1, 4, Cfg.hidden_size, device=cuda).to(torch.bfloat16))
+
+
+def moegate_state_dict(cfg, seed=1):
+    """router.* keys of a YvMoEGate (its own initialisation, then a few buffers and the
+    affinity made non-trivial), with graph-builder / importance keys the module skips."""
+    torch.manual_seed(seed)
+    g = YvMoEGate(cfg.hidden_size, cfg.moe_num_experts, top_k=cfg.moe_top_k, dtype=torch.bfloat16,
+                  cfg=cfg)
+    with torch.no_grad():
+        g.expert_modal_affinity.normal_(0.0, 0.3)
+        g.expert_bias.normal_(0.0, 0.2)
+        g.hicl_dg_encoder.dg_bias.normal_(0.0, 0.05)
+        for name in ("w_hicl", "w_got", "w_soft", "w_expert_orient"):
+            getattr(g, name).fill_(0.5)
+    sd = {"router." + k: v for k, v in g.state_dict().items()}
+    sd["router.got_graph_builder.q_proj.weight"] = torch.zeros(cfg.hidden_size, cfg.hidden_size)
+    sd["router.importance_proj.0.weight"] = torch.zeros(cfg.hidden_size // 4, cfg.hidden_size)
+    return sd
+
+
+def _moegate_oracle_check(layer, x, oracle, skip, modal_id=None, route_logits=None):
+    """GPU logits vs float64, routing bit-exact given the routed logits, output vs the oracle
+    layer on those logits, loss vs the oracle's."""
+    g = layer.router
+    x2d = x.reshape(-1, x.shape[-1])
+    p = mg.params_from_state_dict(g.state_dict(), torch.bfloat16, soft_temperature=g.soft_moe_temperature)
+    og = mg.moegate_forward(x.cpu(), p, layer.top_k, modal_id=None if modal_id is None else modal_id.cpu())
+    lg = g.last_logits.cpu().numpy()
+    ref = og["logits"].numpy()
+    assert float(np.abs(lg - ref).max()) <= 1e-4 * max(1.0, float(np.abs(ref).max()))
+    assert float(g._last_loss_f32) == pytest.approx(og["loss"], rel=1e-4, abs=1e-7)
+    routed = lg if route_logits is None else route_logits
+    r = oracle.route(routed.astype(np.float32), layer.top_k, -1, None)
+    assert np.array_equal(layer.last_routing.indices.cpu().numpy(), r.indices.astype(np.int64))
+    assert np.array_equal(layer.last_routing.perm.cpu().numpy(), r.perm)
+    cpu = layer.experts_packed.to("cpu")
+    params = moe_oracle.LayerParams(
+        hidden=layer.hidden_size, ffn=layer.intermediate_size, num_experts=layer.num_experts,
+        num_shared=layer.num_shared_experts, top_k=layer.top_k,
+        gate_weight=torch.zeros(layer.num_experts, layer.hidden_size), pred=None, bias=None,
+        fixed_shape_mode=True, dynamic_capacity=False, capacity_factor=1.0, min_capacity=0,
+        mix_param=None if layer.shared_expert_weight is None else layer.shared_expert_weight.detach().cpu(),
+        expert_fn=lambda i: cpu.dequantize(i, torch.float32))
+    return moe_oracle.layer_forward(x2d.cpu(), params, logits=routed, cap=-1,
+                                    skip=None if skip is None else skip.reshape(x2d.shape).cpu())
+
+
+def test_deepseek_layer_moegate_router(cuda, oracle):
+    cfg = Cfg()
+    layer = YvDeepSeekMoELayer(cfg, device=cuda, dtype=torch.bfloat16, weight_format="int8").eval()
+    assert isinstance(layer.router, YvMoEGate)
+    sd = reference_state_dict(cfg)
+    sd = {k: v for k, v in sd.items() if not k.startswith("router.")}
+    sd.update(moegate_state_dict(cfg))
+    layer.load_reference_state_dict(sd, strict=True)
+    layer.router._path_moe_stage_size = 1
+    gen = torch.Generator(device=cuda).manual_seed(2)
+    x1 = torch.randn(3, 11, cfg.hidden_size, device=cuda, generator=gen).to(torch.bfloat16)
+    x2 = torch.randn(3, 11, cfg.hidden_size, device=cuda, generator=gen).to(torch.bfloat16)
+    modal = torch.tensor([1, 4, 0], device=cuda)
+    print("module moegate router", flush=True)
+    out1, loss1 = layer(x1, modal_id=modal)
+    torch.cuda.synchronize()
+    o1 = _moegate_oracle_check(layer, x1, oracle, None, modal_id=modal)
+    out1 = out1.reshape(-1, cfg.hidden_size).cpu()
+    assert cosine(out1, o1["out"]) >= 0.9999
+    assert float((out1.double() - o1["out"].double()).abs().max()) <= 2e-2
+    assert loss1.dtype == torch.bfloat16 and float(loss1) > 0
+    skip1 = layer._skip_buffer.clone()
+    out2, _ = layer(x2)                     # skip residual from call 1
+    torch.cuda.synchronize()
+    o2 = _moegate_oracle_check(layer, x2, oracle, skip1)
+    out2 = out2.reshape(-1, cfg.hidden_size).cpu()
+    assert cosine(out2, o2["out"]) >= 0.9999
+    assert float((out2.double() - o2["out"].double()).abs().max()) <= 2e-2
+
+
+def test_moegate_layer_path_moe_stage(cuda, oracle):
+    cfg = Cfg()
+    cfg.moe_shared_experts = 0
+    layer = YvDeepSeekMoELayer(cfg, device=cuda, dtype=torch.bfloat16, weight_format="bf16").eval()
+    sd = reference_state_dict(cfg)
+    sd = {k: v for k, v in sd.items() if not k.startswith("router.")}
+    sd.update(moegate_state_dict(cfg, seed=5))
+    layer.load_reference_state_dict(sd, strict=True)
+    assert layer.router._path_moe_stage_size == 4
+    gen = torch.Generator(device=cuda).manual_seed(3)
+    xs = [torch.randn(2, 8, cfg.hidden_size, device=cuda, generator=gen).to(torch.bfloat16)
+          for _ in range(5)]
+    first_logits = None
+    for i, x in enumerate(xs):
+        out, loss = layer(x)
+        torch.cuda.synchronize()
+        lg = layer.router.last_logits.cpu().numpy()
+        if i % 4 == 0:
+            first_logits = lg               # a stage starts: routes on its own logits
+            o = _moegate_oracle_check(layer, x, oracle, None)
+        else:                               # later calls route on the stage's first logits
+            o = _moegate_oracle_check(layer, x, oracle, None, route_logits=first_logits)
+        got = out.reshape(-1, cfg.hidden_size).cpu()
+        assert cosine(got, o["out"]) >= 0.9999, i
