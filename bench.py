@@ -22,6 +22,9 @@ roofline.traffic: HBM bytes per launch of the same kernel, from two rocprofv3 co
 reads for the probe's calibration copy of known size; the measured figures are kept in
 profiles/expert_ffn_cfg2_decode_traffic.json and reported when present.
 
+"moegate": the same layer shape with YvMoEGate, the router the reference's MoE layers build
+(model/moe/layer.py:754-777): the gate alone and the layer with it, at decode and prefill.
+
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
        python bench.py --pmc-probe {cfg2,cfg3}   (launches only, for counter runs)
 """
@@ -49,6 +52,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--prefill-steps", type=int, default=20)
+    ap.add_argument("--no-moegate", action="store_true",
+                    help="skip the YvMoEGate router and the layer built with it")
     ap.add_argument("--pmc-probe", choices=["cfg2", "cfg3"], default=None,
                     help="run the calibration copy and 5 expert-FFN launches, nothing timed")
     return ap.parse_args()
@@ -124,6 +129,77 @@ def ffn_work(spec, n_tokens, routing):
     nbytes = wbytes + n_tokens * spec.hidden * 2 + rows * spec.hidden * 2
     flops = 6 * spec.hidden * spec.ffn * rows
     return {"bytes": nbytes, "weight_bytes": wbytes, "flops": flops, "active_experts": active}
+
+
+def time_calls(fn, steps, warmup):
+    """Average duration of fn() over `steps` calls, HIP events on the current stream."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    stream = torch.cuda.current_stream()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(steps):
+        fn()
+    b.record(stream)
+    b.synchronize()
+    return a.elapsed_time(b) / 1e3 / steps
+
+
+def moegate_bench(w, mix, steps, prefill_steps, lengths):
+    """YvMoEGate (the router the reference's MoE layers build) at the cfg2 layer shape: the
+    gate alone (logits, loss and routing, yvmoe_moegate_forward) at decode and prefill, and
+    the layer with it as router (yvmoe_forward_moegate). Random module initialisation
+    (seeded), synthetic x."""
+    import torch
+    from pisceslx_amd import _lib
+    from pisceslx_amd import functional as yvf
+    from pisceslx_amd.gate import YvMoEGate
+    spec = w.spec
+    H, E, k = spec.hidden, spec.num_experts, spec.top_k
+    dev = w.x.device
+    torch.manual_seed(0)
+    g = YvMoEGate(H, E, top_k=k, device=dev, dtype=torch.bfloat16).eval()
+    res = {"workload": "cfg2 layer shape (hidden 4096, 64 experts, top-6), YvMoEGate router with "
+                       "all four auxiliary heads, random seeded weights"}
+    for name, N, n_steps in (("decode", w.n_tokens, steps), ("prefill", sum(lengths), prefill_steps)):
+        gen = torch.Generator(device=dev).manual_seed(3)
+        x = torch.randn(N, H, device=dev, generator=gen).to(torch.bfloat16)
+        seq = 1 if name == "decode" else N  # decode: B x 1 tokens; prefill: one packed sequence
+        st = g.gate_state(_lib.ACT_BF16, seq)
+        P = st.w_proj.shape[0]
+        ws = torch.empty(max(256, int(_lib.lib().yvmoe_forward_moegate_workspace_bytes(
+            N, _lib.ACT_BF16, k, __import__("ctypes").byref(st.struct()),
+            __import__("ctypes").byref(w.experts.struct())))), dtype=torch.uint8, device=dev)
+        t_gate = time_calls(lambda: yvf.moegate_forward(x, st, k, workspace=ws), n_steps, 3)
+        t_layer = time_calls(lambda: yvf.moe_forward_moegate(x, st, k, w.experts, mix, None,
+                                                              workspace=ws), n_steps, 3)
+        wbytes = P * H * 2
+        entry = {"tokens": N, "gate_ms_per_call": round(t_gate * 1e3, 4),
+                 "gate_tokens_per_s": round(N / t_gate, 1),
+                 "layer_ms_per_step": round(t_layer * 1e3, 4),
+                 "layer_tokens_per_s": round(N / t_layer, 1),
+                 "projection_rows": P}
+        if name == "decode":
+            nbytes = wbytes + N * H * 2 + H * 4 * 4 + N * E * 4
+            achieved = nbytes / t_gate / 1e9
+            entry["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                                 "kernel": "whole yvmoe_moegate_forward call (projection GEMM, "
+                                           "per-token kernel, loss, routing)",
+                                 "algorithmic_bytes": nbytes}
+        else:
+            flops = 2 * N * H * P
+            tf = flops / t_gate / 1e12
+            entry["roofline"] = {"bound": "mfma", "achieved": round(tf, 1), "peak": BF16_PEAK_TFLOPS,
+                                 "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                                 "kernel": "whole yvmoe_moegate_forward call (projection GEMM, "
+                                           "per-token kernel, loss, routing)",
+                                 "algorithmic_flops": flops}
+        res[name] = entry
+        del x, ws
+    return res
 
 
 def cpu_baseline(w, budget_s=30.0):
@@ -227,6 +303,8 @@ def main():
                          "ms_per_launch": round(tpf * 1e3, 4), "algorithmic_flops": wp["flops"]},
         }
         del xp, skip_p, wsp
+    if not args.no_moegate:
+        result["moegate"] = moegate_bench(w, mix, args.steps, args.prefill_steps, seq_lengths("cfg3", 0))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)
