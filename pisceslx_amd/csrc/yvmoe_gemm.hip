@@ -1304,6 +1304,13 @@ int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, flo
     p.ldo = ld;
     p.nrows = N;
     const int wf = (act == YVMOE_ACT_F32) ? YVMOE_W_F32 : YVMOE_W_BF16;
+    if (N > kSmallRouteTok && dense_tiled(act, N, p.ncols, r->hidden)) {
+        // large batches with a 256-multiple operand width (E <= 64 with bf16 activations):
+        // the LDS-tiled MFMA form, no K split
+        p.kchunk = r->hidden;
+        p.out = out;
+        return tile_dispatch<EPI_F32>(YVMOE_W_BF16, p, ceil_div(N, TBM), st, "router_gemm");
+    }
     const int ks = router_ksplit(N, r->num_experts, act, r->hidden);
     p.kchunk = r->hidden / ks;
     if (ks == 1 || partials == nullptr) {

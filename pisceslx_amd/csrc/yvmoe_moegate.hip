@@ -592,39 +592,53 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
 
 // loss = alpha · Σ_e (mean_n score - 1/E)² + capacity term + z_alpha · mean(logits²)
 //        + 0.01 · (mean_n Σ_e soft - budget)²   (gate.py:433-444, :556-610)
-// Thread c sums column c of the per-work-group sums in group order (16 loads in flight), then
-// the load-balance sum over experts is one wave reduction per wave and the waves in order.
+// Column c of the per-work-group sums is summed by P threads (contiguous group ranges, 32
+// loads in flight each) and the P partial sums in order; the load-balance sum over experts is
+// one wave reduction per wave and the waves in order.
 __global__ __launch_bounds__(1024) void moegate_loss_kernel(const float* __restrict__ part, int G,
                                                             int E, int N, float lb_alpha,
                                                             float z_alpha, float budget,
                                                             float cap_loss, int has_soft,
                                                             float* __restrict__ loss) {
+    __shared__ float psum[1024];
     __shared__ float col[YVMOE_MAX_EXPERTS + 2];
     __shared__ float red[16];
-    const int c = threadIdx.x, lane = c & 63, wave = c >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int cp = 1;
+    while (cp < E + 2) cp <<= 1;
+    const int P = 1024 / cp;  // threads per column (>= 2: E + 2 <= 258)
+    const int c = tid / P, p = tid % P;
+    const int chunk = (G + P - 1) / P;
+    float sum = 0.f;
     if (c < E + 2) {
         const float* pc = part + (long long)c * G;
-        float sum = 0.f;
-        for (int g0 = 0; g0 < G; g0 += 16) {
-            float v[16];
+        const int g1 = min(G, (p + 1) * chunk);
+        for (int g0 = p * chunk; g0 < g1; g0 += 32) {
+            float v[32];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) v[i] = g0 + i < G ? pc[g0 + i] : 0.f;
+            for (int i = 0; i < 32; ++i) v[i] = g0 + i < g1 ? pc[g0 + i] : 0.f;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) sum += v[i];
+            for (int i = 0; i < 32; ++i) sum += v[i];
         }
-        col[c] = sum;
+    }
+    psum[tid] = sum;
+    __syncthreads();
+    if (tid < E + 2) {
+        float s = psum[tid * P];
+        for (int i = 1; i < P; ++i) s += psum[tid * P + i];
+        col[tid] = s;
     }
     __syncthreads();
     const float fn = (float)N;
     float d = 0.f;
-    if (c < E) {
-        d = col[c] / fn - 1.f / (float)E;
+    if (tid < E) {
+        d = col[tid] / fn - 1.f / (float)E;
         d = d * d;
     }
     d = wave_sum(d);
     if (lane == 0) red[wave] = d;
     __syncthreads();
-    if (c == 0) {
+    if (tid == 0) {
         float lb = red[0];
         for (int w = 1; w < 16; ++w) lb += red[w];
         float total = lb_alpha * lb + cap_loss + z_alpha * (col[E] / ((float)N * (float)E));

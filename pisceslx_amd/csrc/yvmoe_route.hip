@@ -761,11 +761,6 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
     }
 }
 
-__global__ void copy_f32_kernel(const float* __restrict__ a, float* __restrict__ b, int n) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) b[i] = a[i];
-}
-
 }  // namespace
 
 int route_launch(const float* logits, int ld, const float* pred, int pred_ld, int N,
@@ -835,10 +830,12 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
         YV_LAUNCH_CHECK("route_scan");
         return YVMOE_OK;
     }
+    // fixed mode has no trim: the top-k kernel's weights are the final ones
+    float* wdst = fixed ? out->weights : w0;
 #define YV_TOPK(NVV)                                                                        \
     route_topk_kernel<NVV><<<nb, 1024, 0, st>>>(logits, ld, r->bias, use_pred, pred_ld,      \
                                                 pred_terms, r->b1, r->w2, r->b2, N, E, k,    \
-                                                out->indices, topp, w0, allowed, blockhist, \
+                                                out->indices, topp, wdst, allowed, blockhist, \
                                                 blocksum)
     if (E <= 16) YV_TOPK(1);
     else if (E <= 64) YV_TOPK(4);
@@ -859,10 +856,6 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
         YV_LAUNCH_CHECK("capacity_trim");
         renorm_kernel<<<ceil_div(N, 256), 256, 0, st>>>(w0, allowed, N, k, out->weights);
         YV_LAUNCH_CHECK("renorm");
-    } else {
-        const int n = N * k;
-        copy_f32_kernel<<<ceil_div(n, 256), 256, 0, st>>>(w0, out->weights, n);
-        YV_LAUNCH_CHECK("copy_weights");
     }
     return YVMOE_OK;
 }
