@@ -30,7 +30,7 @@ import torch.nn.functional as F
 from . import _lib
 from . import functional as yvf
 from .gate import YvMoEGate, YvStableMoEGate
-from .quant import ExpertPacker, FORMAT_BY_NAME, PackedExperts
+from .quant import ExpertPacker, FORMAT_BY_NAME, FORMAT_NAMES, PackedExperts
 
 
 def _kaiming_uniform(out_f: int, in_f: int, generator=None, device=None) -> torch.Tensor:
@@ -143,6 +143,29 @@ class YvDynamicMoELayer(nn.Module):
         router_sd = {k[len("router."):]: v for k, v in sd.items() if k.startswith("router.")}
         if router_sd:
             self.router.load_state_dict(router_sd, strict=strict)
+
+    def load_packed(self, packed) -> None:
+        """Load a packed layer: a file written by ``pisceslx_amd.checkpoint.convert`` (read onto
+        the layer's device) or a ``checkpoint.PackedLayer``."""
+        from .checkpoint import PackedLayer, load_packed
+        dev = self.router.gate.weight.device
+        pl = packed if isinstance(packed, PackedLayer) else load_packed(packed, device=dev)
+        self.set_experts(pl.experts.to(dev))
+        if self.shared_expert_weight is not None and pl.shared_expert_weight is not None:
+            with torch.no_grad():
+                self.shared_expert_weight.copy_(pl.shared_expert_weight)
+        if pl.router:
+            self.router.load_state_dict(pl.router, strict=False)
+
+    def load_reference_checkpoint(self, path: str, prefix: str) -> None:
+        """Load this layer's keys from a whole reference checkpoint (``.pt`` / ``.bin`` /
+        ``.safetensors``, full-precision or reference-quantized experts), packing on the
+        layer's device in its weight format."""
+        from .checkpoint import StateSource, convert_layer, PackedLayer
+        dev = self.router.gate.weight.device
+        experts, router, sw = convert_layer(StateSource(path), prefix, FORMAT_NAMES[self.weight_format],
+                                            device=dev)
+        self.load_packed(PackedLayer(experts, router, sw, {}))
 
     # ------------------------------------------------------------ forward
     def _mix(self) -> Optional[torch.Tensor]:

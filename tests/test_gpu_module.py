@@ -234,3 +234,28 @@ def test_moegate_layer_path_moe_stage(cuda, oracle):
             o = _moegate_oracle_check(layer, x, oracle, None, route_logits=first_logits)
         got = out.reshape(-1, cfg.hidden_size).cpu()
         assert cosine(got, o["out"]) >= 0.9999, i
+
+
+def test_layer_from_packed_checkpoint(cuda, tmp_path):
+    """A reference checkpoint converted offline and loaded gives the same forward as the layer
+    loaded from the state dict directly (same packed bytes)."""
+    from pisceslx_amd import checkpoint as ck
+    cfg = Cfg()
+    sd = {"layers.0.mlp." + k: v for k, v in reference_state_dict(cfg, seed=4).items()}
+    src = str(tmp_path / "model.pt")
+    torch.save({"model": sd}, src)
+    dst = str(tmp_path / "layer0.safetensors")
+    ck.convert(src, dst, "layers.0.mlp.", "int8")
+    a = YvDeepSeekMoELayer(cfg, device=cuda, dtype=torch.bfloat16, weight_format="int8",
+                           router="stable").eval()
+    a.load_packed(dst)
+    b = YvDeepSeekMoELayer(cfg, device=cuda, dtype=torch.bfloat16, weight_format="int8",
+                           router="stable").eval()
+    b.load_reference_state_dict(reference_state_dict(cfg, seed=4))
+    x = torch.randn(2, 13, cfg.hidden_size, device=cuda,
+                    generator=torch.Generator(device=cuda).manual_seed(5)).to(torch.bfloat16)
+    print("packed checkpoint layer", flush=True)
+    oa, _ = a(x)
+    ob, _ = b(x)
+    torch.cuda.synchronize()
+    assert torch.equal(oa, ob)
