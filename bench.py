@@ -25,6 +25,9 @@ profiles/expert_ffn_cfg2_decode_traffic.json and reported when present.
 "moegate": the same layer shape with YvMoEGate, the router the reference's MoE layers build
 (model/moe/layer.py:754-777): the gate alone and the layer with it, at decode and prefill.
 
+"rmsnorm": the MoE input norms of the hybrid block (two RMSNorms in one pass) at the decode
+and prefill token counts, HBM roofline of the kernel.
+
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
        python bench.py --pmc-probe {cfg2,cfg3}   (launches only, for counter runs)
 """
@@ -54,6 +57,7 @@ def parse():
     ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--no-moegate", action="store_true",
                     help="skip the YvMoEGate router and the layer built with it")
+    ap.add_argument("--no-norm", action="store_true", help="skip the MoE input RMSNorm timing")
     ap.add_argument("--pmc-probe", choices=["cfg2", "cfg3"], default=None,
                     help="run the calibration copy and 5 expert-FFN launches, nothing timed")
     return ap.parse_args()
@@ -202,6 +206,46 @@ def moegate_bench(w, mix, steps, prefill_steps, lengths):
     return res
 
 
+def norm_bench(w, steps, lengths):
+    """The MoE input norms of the hybrid block (norm_fusion then norm_mlp, one yvmoe_rmsnorm
+    pass) at hidden 4096, decode and prefill token counts. Launches are captured in a HIP
+    graph of `reps` kernels so the per-kernel time excludes Python's launch cost; the roofline
+    prices one launch at its algorithmic bytes: x read once, y written once, two weights."""
+    import torch
+    from pisceslx_amd import functional as yvf
+    H = w.spec.hidden
+    dev = w.x.device
+    gen = torch.Generator(device=dev).manual_seed(5)
+    wts = [(1.0 + 0.1 * torch.randn(H, device=dev, generator=gen)).to(torch.bfloat16) for _ in range(2)]
+    norms = [(wt, None, 1e-6) for wt in wts]
+    res = {"workload": "two RMSNorms in sequence (YvHybridBlock norm_fusion, norm_mlp), hidden 4096, "
+                       "bf16, one pass"}
+    for name, N in (("decode", w.n_tokens), ("prefill", sum(lengths))):
+        x = torch.randn(N, H, device=dev, generator=gen).to(torch.bfloat16)
+        y = torch.empty_like(x)
+        reps = 50
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(side):
+            yvf.rms_norm(x, norms, out=y)          # warm the launch path outside the capture
+        torch.cuda.current_stream(dev).wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(reps):
+                yvf.rms_norm(x, norms, out=y)
+        t = time_calls(graph.replay, max(3, steps // 10), 2) / reps
+        nbytes = 2 * N * H * 2 + 2 * H * 2
+        achieved = nbytes / t / 1e9
+        res[name] = {"tokens": N, "us_per_call": round(t * 1e6, 3),
+                     "timing": "HIP graph of 50 launches, per node (includes the graph's per-node "
+                               "launch cost, which dominates a kernel of a few us)",
+                     "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                                  "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                                  "kernel": "rmsnorm_kernel (2 norms)", "algorithmic_bytes": nbytes}}
+        del graph, x, y
+    return res
+
+
 def cpu_baseline(w, budget_s=30.0):
     """The CPU oracle (reference algorithm restated with torch on the host), bounded."""
     import torch
@@ -305,6 +349,8 @@ def main():
         del xp, skip_p, wsp
     if not args.no_moegate:
         result["moegate"] = moegate_bench(w, mix, args.steps, args.prefill_steps, seq_lengths("cfg3", 0))
+    if not args.no_norm:
+        result["rmsnorm"] = norm_bench(w, args.steps, seq_lengths("cfg3", 0))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)

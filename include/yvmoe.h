@@ -30,6 +30,10 @@
  *   yvmoe_moegate_forward-> YvMoEGate.forward in eval mode (logits, loss and routing)
  *   yvmoe_forward_moegate-> YvDynamicMoELayer.forward with its YvMoEGate router
  *                           model/moe/layer.py:867-963 (inference)
+ *   yvmoe_rmsnorm        -> YvRMSNorm.forward model/core/norms.py:206-208 via
+ *                           fused_rms_norm opss/kernels/fused_rms_norm.py:42; two in a
+ *                           row = YvHybridBlock's norm_fusion then norm_mlp
+ *                           model/core/hybrid.py:1359, :1310
  */
 #ifndef YVMOE_H
 #define YVMOE_H
@@ -281,6 +285,29 @@ int32_t yvmoe_moegate_forward(const void* x, int32_t act_dtype, int32_t n_tokens
                               const yvmoe_moegate* gate, const int32_t* modal_id, int32_t top_k,
                               float* logits, float* loss, yvmoe_routing* routing,
                               void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * One YvRMSNorm (model/core/norms.py:178-208): weight [H], bias [H] or NULL, eps.
+ */
+typedef struct yvmoe_rmsnorm_params {
+    const void* weight;
+    const void* bias;
+    float eps;
+    int32_t reserved;
+} yvmoe_rmsnorm_params;
+
+/*
+ * RMSNorm of the MoE input: n_norms (1 or 2) YvRMSNorms applied in sequence, each as the
+ * reference's CUDA path computes it (fused_rms_norm, opss/kernels/fused_rms_norm.py:42,
+ * through YvNorms._norm_forward, model/core/norms.py:964-1007): per row rms = sqrt(Σx²/H + eps)
+ * in fp32, (x / rms) * weight rounded once to the activation dtype, then + bias (rounded
+ * again) when bias is not NULL (norms.py:998-999). Two norms cover the MoE input of
+ * YvHybridBlock, norm_mlp(norm_fusion(h)) (model/core/hybrid.py:1359, :1310), in one pass.
+ * x, weights, biases and out in the activation dtype, [N][H] row-major, H % 8 == 0; out may
+ * alias x.
+ */
+int32_t yvmoe_rmsnorm(const void* x, int32_t act_dtype, int32_t n_tokens, int32_t hidden,
+                      const yvmoe_rmsnorm_params* norms, int32_t n_norms, void* out, void* stream);
 
 /*
  * The whole layer with YvMoEGate as its router, as YvDynamicMoELayer builds it

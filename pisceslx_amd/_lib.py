@@ -52,6 +52,7 @@ EXPORTED_SYMBOLS = (
     "yvmoe_moegate_forward",
     "yvmoe_forward_moegate_workspace_bytes",
     "yvmoe_forward_moegate",
+    "yvmoe_rmsnorm",
 )
 
 # YvMoEGate auxiliary heads (YVMOE_HEAD_*)
@@ -103,6 +104,16 @@ class Routing(ctypes.Structure):
         ("perm", ctypes.c_void_p),
         ("pos", ctypes.c_void_p),
         ("capacity", ctypes.c_void_p),
+    ]
+
+
+class RMSNormParams(ctypes.Structure):
+    """yvmoe_rmsnorm_params (include/yvmoe.h)."""
+    _fields_ = [
+        ("weight", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
+        ("eps", ctypes.c_float),
+        ("reserved", ctypes.c_int32),
     ]
 
 
@@ -177,6 +188,8 @@ def _declare(l: ctypes.CDLL) -> None:
     l.yvmoe_forward_moegate.argtypes = [vp, i32, i32, ctypes.POINTER(MoEGate), vp, i32, vp,
                                         ctypes.POINTER(ExpertWeights), vp, vp, vp, vp,
                                         ctypes.POINTER(Routing), vp, vp, vp, sz, vp]
+    l.yvmoe_rmsnorm.restype = i32
+    l.yvmoe_rmsnorm.argtypes = [vp, i32, i32, i32, ctypes.POINTER(RMSNormParams), i32, vp, vp]
     l.yvmoe_forward.restype = i32
     l.yvmoe_forward.argtypes = [vp, i32, i32, ctypes.POINTER(Router), ctypes.POINTER(ExpertWeights),
                                 vp, vp, vp, vp, ctypes.POINTER(Routing), vp, sz, vp]

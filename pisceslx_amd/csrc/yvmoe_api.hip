@@ -427,4 +427,30 @@ int32_t yvmoe_forward_moegate(const void* x, int32_t act_dtype, int32_t n_tokens
                           shared_out, st);
 }
 
+int32_t yvmoe_rmsnorm(const void* x, int32_t act_dtype, int32_t n_tokens, int32_t hidden,
+                      const yvmoe_rmsnorm_params* norms, int32_t n_norms, void* out, void* stream) {
+    clear_error();
+    YV_REQUIRE(act_dtype == YVMOE_ACT_F32 || act_dtype == YVMOE_ACT_BF16, YVMOE_ERR_DTYPE,
+               "unknown activation dtype %d", act_dtype);
+    YV_REQUIRE(n_tokens >= 0 && hidden > 0 && hidden % 8 == 0, YVMOE_ERR_SHAPE,
+               "n_tokens=%d, hidden=%d (a positive multiple of 8)", n_tokens, hidden);
+    YV_REQUIRE(norms != nullptr && (n_norms == 1 || n_norms == 2), YVMOE_ERR_ARG,
+               "n_norms=%d (1 or 2 norms)", n_norms);
+    NormChain nc{};
+    for (int n = 0; n < n_norms; ++n) {
+        YV_REQUIRE(norms[n].weight != nullptr, YVMOE_ERR_ARG, "norm %d: NULL weight", n);
+        YV_REQUIRE(((uintptr_t)norms[n].weight | (uintptr_t)norms[n].bias) % 16 == 0,
+                   YVMOE_ERR_ARG, "norm %d: weight and bias must be 16-byte aligned", n);
+        YV_REQUIRE(norms[n].eps >= 0.f, YVMOE_ERR_ARG, "norm %d: eps=%g < 0", n, norms[n].eps);
+        nc.w[n] = norms[n].weight;
+        nc.b[n] = norms[n].bias;
+        nc.eps[n] = norms[n].eps;
+    }
+    if (n_tokens == 0) return YVMOE_OK;
+    YV_REQUIRE(x && out, YVMOE_ERR_ARG, "NULL pointer");
+    YV_REQUIRE(((uintptr_t)x | (uintptr_t)out) % 16 == 0, YVMOE_ERR_ARG,
+               "x and out must be 16-byte aligned");
+    return rmsnorm_launch(x, act_dtype, n_tokens, hidden, nc, n_norms, out, (hipStream_t)stream);
+}
+
 }  // extern "C"

@@ -197,6 +197,14 @@ int moegate_proj_rows(const yvmoe_moegate* g);
 GateWs gate_ws(int N, int act, const yvmoe_moegate* g);
 int moegate_launch(const void* x, int act, int N, const yvmoe_moegate* g, const int* modal_id,
                    float* logits, float* loss, char* ws, hipStream_t st);
+// RMSNorm (yvmoe_norm.hip): nn (1 or 2) norms in sequence, one wavefront per row; y may alias x.
+struct NormChain {
+    const void* w[2];
+    const void* b[2];
+    float eps[2];
+};
+int rmsnorm_launch(const void* x, int act, int N, int H, const NormChain& nc, int nn, void* y,
+                   hipStream_t st);
 int combine_launch(const void* y, int act, int N, int H, int k, int S,
                    const yvmoe_routing* routing, const float* mix, const void* skip,
                    void* out, void* shared_out, hipStream_t st);

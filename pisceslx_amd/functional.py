@@ -353,3 +353,39 @@ def moe_forward_moegate(x2d: torch.Tensor, gate: MoEGateState, top_k: int, exper
         logits.data_ptr() if N > 0 else None, loss.data_ptr(), workspace.data_ptr(),
         workspace.numel(), _stream(dev)), "yvmoe_forward_moegate")
     return out, shared_out, routing, logits, loss, workspace
+
+
+def rms_norm(x: torch.Tensor, norms, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """RMSNorm over the last dimension, one or two norms in sequence in one pass.
+
+    ``norms`` is a sequence of (weight, bias or None, eps); two entries apply the second norm to
+    the first one's output rounded to x's dtype (YvHybridBlock's norm_fusion then norm_mlp,
+    model/core/hybrid.py:1359, :1310). Each norm follows fused_rms_norm
+    (opss/kernels/fused_rms_norm.py:42): fp32 sum of squares, (x / sqrt(Σx²/H + eps)) * weight
+    rounded once, + bias rounded again (model/core/norms.py:998-999). ``out`` may be x.
+    """
+    norms = list(norms)
+    if len(norms) not in (1, 2):
+        raise ValueError("rms_norm takes one or two norms")
+    H = x.shape[-1]
+    ts = [x] + [t for w, b, _ in norms for t in (w, b)]
+    dev = _require_cuda(*ts, out)
+    act = _act(x.dtype)
+    for w, b, _ in norms:
+        for t in (w, b):
+            if t is not None and (t.dtype != x.dtype or t.numel() != H):
+                raise ValueError(f"norm weight/bias must be {x.dtype} [{H}]")
+    if out is None:
+        out = torch.empty_like(x)
+    elif out.shape != x.shape or out.dtype != x.dtype:
+        raise ValueError("out must match x")
+    N = x.numel() // H if H else 0
+    params = (_lib.RMSNormParams * len(norms))()
+    for i, (w, b, eps) in enumerate(norms):
+        params[i].weight = w.data_ptr()
+        params[i].bias = _ptr(b)
+        params[i].eps = float(eps)
+    _lib.check(_lib.lib().yvmoe_rmsnorm(x.data_ptr() if N > 0 else None, act, N, H, params,
+                                        len(norms), out.data_ptr() if N > 0 else None,
+                                        _stream(dev)), "yvmoe_rmsnorm")
+    return out
