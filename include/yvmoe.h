@@ -58,7 +58,8 @@ typedef enum {
 /* activation dtype of x, the expert intermediates and the output */
 typedef enum { YVMOE_ACT_F32 = 0, YVMOE_ACT_BF16 = 1 } yvmoe_act_dtype;
 
-/* expert weight formats (all [out][in] row-major per expert, like nn.Linear.weight) */
+/* expert weight formats (the values of nn.Linear.weight [out][in] per expert; storage order
+ * below, at yvmoe_expert_weights) */
 typedef enum {
     YVMOE_W_F32 = 0,  /* fp32 weights, no scales (activations must be fp32) */
     YVMOE_W_BF16 = 1, /* bf16 weights, no scales */
@@ -83,6 +84,13 @@ typedef enum {
  * experts.{e}.{gate,up,down}_proj.weight and shared_experts.{s}.expert.*).
  *   w_gate, w_up : [E+S][F][H] elements of the format (INT4: [E+S][F][H/2] bytes)
  *   w_down       : [E+S][H][F]                         (INT4: [E+S][H][F/2] bytes)
+ *   Storage order of w_*: F32 row-major; BF16, INT8, INT4 and FP8 in 16-row x 64-column
+ *   blocks, each block contiguous, blocks ordered [out/16][in/64]. Inside a block, piece
+ *   (g, r) — row r (0..15), columns 16 g .. 16 g + 15 (g = 0..3) — starts at byte
+ *   (16 g + r) * 16 (INT8, FP8: 16 codes; INT4: at (16 g + r) * 8, 8 bytes, low nibble =
+ *   even column); BF16 pieces put columns 16 g .. 16 g + 7 at (16 g + r) * 16 and
+ *   16 g + 8 .. 16 g + 15 at 1024 + (16 g + r) * 16. Block bytes: 1024 (INT8, FP8), 512
+ *   (INT4), 2048 (BF16). pisceslx_amd/quant.py block_matrix() writes this order.
  *   s_gate, s_up : INT8 bf16 [E+S][F]; INT4 bf16 [E+S][F][H/128];
  *                  FP8 fp32 [E+S][F/128][H/128]; NULL otherwise
  *   s_down       : INT8 bf16 [E+S][H]; INT4 bf16 [E+S][H][F/128];

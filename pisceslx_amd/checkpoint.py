@@ -43,7 +43,7 @@ import torch
 
 from .quant import FORMAT_BY_NAME, FORMAT_NAMES, ExpertPacker, PackedExperts
 
-PACKED_VERSION = "1"
+PACKED_VERSION = "2"  # 2: expert matrices in 16-row x 64-column blocks (quant.block_matrix)
 _UNWRAP_KEYS = ("model_state_dict", "model", "state_dict")
 
 
@@ -243,7 +243,8 @@ def load_packed(path: str, device="cuda") -> PackedLayer:
     with safe_open(path, framework="pt", device="cpu") as f:
         meta = dict(f.metadata() or {})
     if meta.get("pisceslx_amd.packed") != PACKED_VERSION:
-        raise ValueError(f"{path}: not a packed expert file (version {meta.get('pisceslx_amd.packed')})")
+        raise ValueError(f"{path}: not a packed expert file of layout version {PACKED_VERSION} "
+                         f"(found {meta.get('pisceslx_amd.packed')}); convert the checkpoint again")
     t = load_file(path, device=str(device))
     experts = PackedExperts(FORMAT_BY_NAME[meta["format"]], int(meta["num_routed"]),
                             int(meta["num_shared"]), int(meta["hidden"]), int(meta["ffn"]),

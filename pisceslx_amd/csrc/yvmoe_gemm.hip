@@ -102,9 +102,16 @@ union Frag16 {  // 16 bf16 = two MFMA operands
 template <int WF>
 struct BLoad;
 
+// Expert matrices are stored in 16-row x 64-column blocks (pisceslx_amd/quant.py
+// block_matrix): lane l = 16 g + r of a 16-column group reads piece (g, r) of each block, a
+// contiguous 16 bytes per lane (8 for int4; bf16 pieces are split in two halves 1 KB apart).
+// bptr() is the lane's address of its piece in the first block of column group n / 16 from
+// K offset kbeg; load_blk() reads the piece of the ks-th 64-wide block after it. Dense
+// weights (router, gate projections) stay row-major and use ptr() / load().
 template <>
 struct BLoad<YVMOE_W_BF16> {
     typedef Frag16 Raw;
+    static constexpr int BLK = 2048;
     static __device__ __forceinline__ const char* ptr(const void* base, long long e_off, int n,
                                                       int K, int kl) {
         return (const char*)base + (e_off + (long long)n * K + kl) * 2;
@@ -114,18 +121,35 @@ struct BLoad<YVMOE_W_BF16> {
         r.u[0] = q[0];
         r.u[1] = q[1];
     }
+    static __device__ __forceinline__ const char* bptr(const void* base, long long e_off, int n,
+                                                       int K, int kbeg, int lane) {
+        return (const char*)base + e_off * 2 + ((long long)(n >> 4) * (K / 64) + kbeg / 64) * BLK +
+               lane * 16;
+    }
+    static __device__ __forceinline__ void load_blk(Raw& r, const char* p, int ks) {
+        r.u[0] = *(const uint4*)(p + (size_t)ks * BLK);
+        r.u[1] = *(const uint4*)(p + (size_t)ks * BLK + 1024);
+    }
     static __device__ __forceinline__ void cvt(const Raw& r, float, Frag16& f) { f = r; }
 };
 
 template <>
 struct BLoad<YVMOE_W_INT8> {
     typedef uint4 Raw;
+    static constexpr int BLK = 1024;
     static __device__ __forceinline__ const char* ptr(const void* base, long long e_off, int n,
                                                       int K, int kl) {
         return (const char*)base + (e_off + (long long)n * K + kl);
     }
     static __device__ __forceinline__ void load(Raw& r, const char* p, int k0) {
         r = *(const uint4*)(p + k0);
+    }
+    static __device__ __forceinline__ const char* bptr(const void* base, long long e_off, int n,
+                                                       int K, int kbeg, int lane) {
+        return (const char*)base + e_off + ((long long)(n >> 4) * (K / 64) + kbeg / 64) * BLK + lane * 16;
+    }
+    static __device__ __forceinline__ void load_blk(Raw& r, const char* p, int ks) {
+        r = *(const uint4*)(p + (size_t)ks * BLK);
     }
     static __device__ __forceinline__ void cvt(const Raw& r, float s, Frag16& f) {
         const unsigned w[4] = {r.x, r.y, r.z, r.w};
@@ -147,6 +171,7 @@ struct BLoad<YVMOE_W_INT8> {
 template <>
 struct BLoad<YVMOE_W_INT4> {
     typedef uint2 Raw;
+    static constexpr int BLK = 512;
     static __device__ __forceinline__ const char* ptr(const void* base, long long e_off, int n,
                                                       int K, int kl) {
         // e_off, n * K and kl count int4 elements (all even): two per byte
@@ -154,6 +179,13 @@ struct BLoad<YVMOE_W_INT4> {
     }
     static __device__ __forceinline__ void load(Raw& r, const char* p, int k0) {
         r = *(const uint2*)(p + k0 / 2);
+    }
+    static __device__ __forceinline__ const char* bptr(const void* base, long long e_off, int n,
+                                                       int K, int kbeg, int lane) {
+        return (const char*)base + e_off / 2 + ((long long)(n >> 4) * (K / 64) + kbeg / 64) * BLK + lane * 8;
+    }
+    static __device__ __forceinline__ void load_blk(Raw& r, const char* p, int ks) {
+        r = *(const uint2*)(p + (size_t)ks * BLK);
     }
     static __device__ __forceinline__ void cvt(const Raw& r, float s, Frag16& f) {
         const unsigned w[2] = {r.x, r.y};
@@ -176,12 +208,20 @@ struct BLoad<YVMOE_W_INT4> {
 template <>
 struct BLoad<YVMOE_W_FP8> {
     typedef uint4 Raw;
+    static constexpr int BLK = 1024;
     static __device__ __forceinline__ const char* ptr(const void* base, long long e_off, int n,
                                                       int K, int kl) {
         return (const char*)base + (e_off + (long long)n * K + kl);
     }
     static __device__ __forceinline__ void load(Raw& r, const char* p, int k0) {
         r = *(const uint4*)(p + k0);
+    }
+    static __device__ __forceinline__ const char* bptr(const void* base, long long e_off, int n,
+                                                       int K, int kbeg, int lane) {
+        return (const char*)base + e_off + ((long long)(n >> 4) * (K / 64) + kbeg / 64) * BLK + lane * 16;
+    }
+    static __device__ __forceinline__ void load_blk(Raw& r, const char* p, int ks) {
+        r = *(const uint4*)(p + (size_t)ks * BLK);
     }
     static __device__ __forceinline__ void cvt(const Raw& r, float s, Frag16& f) {
         const unsigned w[4] = {r.x, r.y, r.z, r.w};
@@ -234,6 +274,7 @@ struct NMat {
 template <int WF, int EPI, int NCB, int MAXRB, int RB = 4, int RA = 2>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
     constexpr int NM = NMat<EPI>::value;
+    constexpr bool BLKD = EPI != EPI_F32;  // expert matrices are blocked, dense ones row-major
     constexpr bool GROUPED = (WF == YVMOE_W_INT4 || WF == YVMOE_W_FP8);
     static_assert(RB % RA == 0, "A ring depth must divide the B ring depth");
     constexpr int R = RB;
@@ -274,8 +315,13 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
         ncol[cb] = col0 + cb * 16 + (lane & 15);
-        bptr[0][cb] = BL::ptr(p.B0, e_off, ncol[cb], p.K, kbeg + kl);
-        if constexpr (NM == 2) bptr[NM - 1][cb] = BL::ptr(p.B1, e_off, ncol[cb], p.K, kbeg + kl);
+        if constexpr (BLKD) {
+            bptr[0][cb] = BL::bptr(p.B0, e_off, ncol[cb], p.K, kbeg, lane);
+            if constexpr (NM == 2) bptr[NM - 1][cb] = BL::bptr(p.B1, e_off, ncol[cb], p.K, kbeg, lane);
+        } else {
+            bptr[0][cb] = BL::ptr(p.B0, e_off, ncol[cb], p.K, kbeg + kl);
+            if constexpr (NM == 2) bptr[NM - 1][cb] = BL::ptr(p.B1, e_off, ncol[cb], p.K, kbeg + kl);
+        }
     }
 
     f32x4 acc[NM][NCB][MAXRB];
@@ -301,7 +347,8 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
         for (int m = 0; m < NM; ++m)
 #pragma unroll
             for (int cb = 0; cb < NCB; ++cb) {
-                BL::load(dst[m][cb], bptr[m][cb], k0);
+                if constexpr (BLKD) BL::load_blk(dst[m][cb], bptr[m][cb], slot_ks);
+                else BL::load(dst[m][cb], bptr[m][cb], k0);
                 if constexpr (GROUPED)
                     sdst[m][cb] = b_scale<WF>(sptr[m], s_off, ncol[cb], p.K, kbeg + k0);
             }
@@ -412,6 +459,7 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
                                             uint4 (&As)[2][16 * MAXRB * (U * 8 + 1)]) {
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
     constexpr bool GROUPED = (WF == YVMOE_W_INT4 || WF == YVMOE_W_FP8);
+    constexpr bool BLKD = EPI != EPI_F32;  // expert matrices are blocked, dense ones row-major
     constexpr int ROWS = 16 * MAXRB;
     constexpr int ROW_U4 = U * 8 + 1;            // uint4 per staged row (U*64 bf16 + pad)
     constexpr int CHUNK_U4 = ROWS * U * 8;       // uint4 of one chunk
@@ -476,7 +524,8 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
         const int c0 = colw + b * 16;
         active[b] = c0 < p.ncols;  // blocks past the last column still stage and sync
         n[b] = min(c0, p.ncols - 16) + (lane & 15);
-        bptr[b] = BL::ptr(mat ? p.B1 : p.B0, e_off, n[b], p.K, kbeg + kl);
+        if constexpr (BLKD) bptr[b] = BL::bptr(mat ? p.B1 : p.B0, e_off, n[b], p.K, kbeg, lane);
+        else bptr[b] = BL::ptr(mat ? p.B1 : p.B0, e_off, n[b], p.K, kbeg + kl);
         scl[b] = b_scale<WF>(S, s_off, n[b], p.K, 0);
     }
 
@@ -502,7 +551,8 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const int ks = min(ks0 + u, nks - 1);
-                    BL::load(bw[b][u], bptr[b], ks * 64);
+                    if constexpr (BLKD) BL::load_blk(bw[b][u], bptr[b], ks);
+                    else BL::load(bw[b][u], bptr[b], ks * 64);
                     if constexpr (GROUPED) sg[b][u] = b_scale<WF>(S, s_off, n[b], p.K, kbeg + ks * 64);
                     else sg[b][u] = scl[b];
                 }
@@ -686,6 +736,8 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     typedef TileCfg<WF> C;
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
     constexpr bool GROUPED = WF == YVMOE_W_FP8;
+    constexpr bool BLKD = EPI != EPI_F32;                              // blocked expert weights
+    constexpr long long B_CHUNK = BLKD ? 1024LL * C::EB : TBK * C::EB;  // bytes per 64-wide step
     static_assert(WF == YVMOE_W_INT8 || WF == YVMOE_W_FP8 || WF == YVMOE_W_BF16,
                   "tiled form covers 1- and 2-byte weight formats");
     __shared__ __attribute__((aligned(1024))) unsigned char lds_a[C::NST][C::A_BYTES];
@@ -726,21 +778,32 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
         const int gr = (row0 + r < seg_end) ? row0 + r : row0;
         a_src[j] = (const char*)p.A + ((long long)map_row(p, gr) * p.lda + lc * 8) * 2;
     }
+    // weight blocks: expert matrices are stored in 16-row x 64-column blocks (1 KB per 1-byte
+    // block, two 1 KB halves per bf16 block) that land in LDS as stored, block after block;
+    // dense weights (EPI_F32) are row-major and land swizzled like the activations
     const char* b_src[C::B_DMA];
 #pragma unroll
     for (int j = 0; j < C::B_DMA; ++j) {
         const int blk = wave * C::B_DMA + j;
-        int r, lc;
-        if constexpr (C::EB == 1) {
-            r = blk * 16 + lane / 4;
-            lc = (lane % 4) ^ ((r >> 1) & 3);
+        if constexpr (BLKD) {
+            const int r16 = (blk / C::EB) * 16, half = blk % C::EB;
+            const void* B = (SWIGLU && r16 >= TBN / 2) ? p.B1 : p.B0;
+            const int nb16 = SWIGLU ? n0 + (r16 & (TBN / 2 - 1)) : n0 + r16;
+            b_src[j] = (const char*)B + e_off * C::EB + (long long)(nb16 >> 4) * (p.K / 64) * B_CHUNK +
+                       half * 1024 + lane * 16;
         } else {
-            r = blk * 8 + lane / 8;
-            lc = (lane % 8) ^ (r & 7) ^ ((r >> 3) & 1);
+            int r, lc;
+            if constexpr (C::EB == 1) {
+                r = blk * 16 + lane / 4;
+                lc = (lane % 4) ^ ((r >> 1) & 3);
+            } else {
+                r = blk * 8 + lane / 8;
+                lc = (lane % 8) ^ (r & 7) ^ ((r >> 3) & 1);
+            }
+            const void* B = (SWIGLU && r >= TBN / 2) ? p.B1 : p.B0;
+            const int n = SWIGLU ? n0 + (r & (TBN / 2 - 1)) : n0 + r;
+            b_src[j] = (const char*)B + (e_off + (long long)n * p.K) * C::EB + lc * 16;
         }
-        const void* B = (SWIGLU && r >= TBN / 2) ? p.B1 : p.B0;
-        const int n = SWIGLU ? n0 + (r & (TBN / 2 - 1)) : n0 + r;
-        b_src[j] = (const char*)B + (e_off + (long long)n * p.K) * C::EB + lc * 16;
     }
 
     // this lane's weight rows in the tile (fragment column l % 16 of each 16-row block)
@@ -781,7 +844,10 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     int b_rd0[2], b_rd1[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-        if constexpr (C::EB == 1) {
+        if constexpr (BLKD) {  // piece (g, r) of the row's block: lane * 16 (second half + 1 KB)
+            b_rd0[nb] = (brow[nb] >> 4) * 1024 * C::EB + lane * 16;
+            b_rd1[nb] = b_rd0[nb] + 1024;
+        } else if constexpr (C::EB == 1) {
             b_rd0[nb] = swz_b(brow[nb], g);
             b_rd1[nb] = 0;
         } else {
@@ -798,7 +864,7 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
         _Pragma("unroll") for (int j = 0; j < C::A_DMA; ++j)                                           \
             dma16(a_src[j] + (size_t)(CHUNK) * TBK * 2, &lds_a[ST][(wave * C::A_DMA + j) * 1024]);     \
         _Pragma("unroll") for (int j = 0; j < C::B_DMA; ++j)                                           \
-            dma16(b_src[j] + (size_t)(CHUNK) * TBK * C::EB, &lds_b[ST][(wave * C::B_DMA + j) * 1024]); \
+            dma16(b_src[j] + (size_t)(CHUNK) * B_CHUNK, &lds_b[ST][(wave * C::B_DMA + j) * 1024]);     \
     } while (0)
 
     YV_TILE_ISSUE(0, 0);

@@ -19,6 +19,15 @@ Formats (one expert weight is an nn.Linear.weight, [out][in] row-major):
 
 These run once at weight-load time (torch on whatever device holds the weights); the
 forward consumes the packed tensors directly.
+
+Packed layout of the expert matrices (bf16, int8, int4 and fp8; fp32 stays row-major):
+16-row x 64-column blocks, each contiguous, blocks ordered row-block major then K. Inside a
+block, piece (g, r) = row r (0..15) and columns 16 g .. 16 g + 15 (g = 0..3) sits at
+(16 g + r) x piece bytes (16 for 1-byte codes, 8 for int4); bf16 blocks hold the first 8
+columns of every piece in their first 1 KB and the last 8 in the second. A wavefront lane
+l = 16 g + r of the GEMM kernels needs exactly piece (g, r) of each block, so every weight
+load of a 16-column group is one contiguous 1 KB (512 B for int4) read
+(:func:`block_matrix`, :func:`unblock_matrix`).
 """
 from __future__ import annotations
 
@@ -97,13 +106,60 @@ def dequantize_fp8(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
     return (v * s.float()[:, None, :, None]).view(out, inn)
 
 
+# ------------------------------------------------------------------ blocked layout
+BLOCKED_FORMATS = (_lib.W_BF16, _lib.W_INT8, _lib.W_INT4, _lib.W_FP8)
+
+
+def _block_view(t: torch.Tensor, fmt: int):
+    """[..., out, row_bytes] (uint8 view) -> the 6-/7-d view whose permutation is the layout."""
+    *lead, out, nb = t.shape
+    if fmt == _lib.W_BF16:       # 64 columns = 128 B per row-block row: [kb][g][h][16 B]
+        return t.reshape(*lead, out // 16, 16, nb // 128, 4, 2, 16)
+    piece = 8 if fmt == _lib.W_INT4 else 16
+    return t.reshape(*lead, out // 16, 16, nb // (4 * piece), 4, piece)
+
+
+def block_matrix(q: torch.Tensor, fmt: int) -> torch.Tensor:
+    """Stored codes [..., out, in-bytes] in row-major order -> the blocked layout (same shape
+    and dtype, elements reordered). out % 16 == 0 and in % 64 == 0 are required."""
+    if fmt not in BLOCKED_FORMATS:
+        return q
+    u = q.contiguous().view(torch.uint8)
+    v = _block_view(u, fmt)
+    n = v.dim()
+    if fmt == _lib.W_BF16:       # (..., ob, r, kb, g, h, b) -> (..., ob, kb, h, g, r, b)
+        o = list(range(n - 6)) + [n - 6, n - 4, n - 2, n - 3, n - 5, n - 1]
+    else:                        # (..., ob, r, kb, g, b) -> (..., ob, kb, g, r, b)
+        o = list(range(n - 5)) + [n - 5, n - 3, n - 2, n - 4, n - 1]
+    return v.permute(*o).contiguous().view(u.shape).view(q.dtype)
+
+
+def unblock_matrix(b: torch.Tensor, fmt: int) -> torch.Tensor:
+    """Inverse of :func:`block_matrix`."""
+    if fmt not in BLOCKED_FORMATS:
+        return b
+    u = b.contiguous().view(torch.uint8)
+    *lead, out, nb = u.shape
+    if fmt == _lib.W_BF16:
+        v = u.reshape(*lead, out // 16, nb // 128, 2, 4, 16, 16)     # (ob, kb, h, g, r, b)
+        n = v.dim()
+        o = list(range(n - 6)) + [n - 6, n - 2, n - 5, n - 3, n - 4, n - 1]
+    else:
+        piece = 8 if fmt == _lib.W_INT4 else 16
+        v = u.reshape(*lead, out // 16, nb // (4 * piece), 4, 16, piece)  # (ob, kb, g, r, b)
+        n = v.dim()
+        o = list(range(n - 5)) + [n - 5, n - 2, n - 4, n - 3, n - 1]
+    return v.permute(*o).contiguous().view(u.shape).view(b.dtype)
+
+
 # ------------------------------------------------------------------ packed expert stack
 @dataclass
 class PackedExperts:
     """Routed experts [0, E) and shared experts [E, E+S) stacked in one format.
 
-    w_gate/w_up [E+S][F][H], w_down [E+S][H][F] (int4: last dim halved, uint8), scales as
-    documented in include/yvmoe.h.
+    w_gate/w_up [E+S][F][H], w_down [E+S][H][F] (int4: last dim halved, uint8) in the
+    blocked layout of :func:`block_matrix` (fp32: row-major), scales row-major as documented
+    in include/yvmoe.h.
     """
 
     format: int
@@ -147,7 +203,7 @@ class PackedExperts:
         fmt = self.format
         res = []
         for w, s in ((self.w_gate, self.s_gate), (self.w_up, self.s_up), (self.w_down, self.s_down)):
-            we = w[expert]
+            we = unblock_matrix(w[expert], fmt)
             if fmt in (_lib.W_F32, _lib.W_BF16):
                 d = we.float()
             elif fmt == _lib.W_INT8:
@@ -208,7 +264,7 @@ class ExpertPacker:
         p = self.packed
         for w, dst, sdst in ((wg, p.w_gate, p.s_gate), (wu, p.w_up, p.s_up), (wd, p.w_down, p.s_down)):
             q, s = quantize_matrix(w.to(dst.device), self.fmt)
-            dst[expert].copy_(q)
+            dst[expert].copy_(block_matrix(q, self.fmt))
             if sdst is not None:
                 sdst[expert].copy_(s)
 

@@ -100,3 +100,41 @@ def test_packer_dequantize_matches_formats(fmt):
             else:
                 bound = b.abs() / 16 + 1e-6                                   # e4m3: 3 mantissa bits
             assert ((a - b).abs() <= bound + 1e-9).all()
+
+
+@pytest.mark.parametrize("fmt", [_lib.W_BF16, _lib.W_INT8, _lib.W_INT4, _lib.W_FP8])
+def test_blocked_layout_addresses(fmt):
+    """block_matrix puts every stored byte at the address include/yvmoe.h documents, and
+    unblock_matrix inverts it (also on a stacked [X][out][in] tensor)."""
+    g = torch.Generator().manual_seed(fmt)
+    out, cols = 48, 192                       # 3 row blocks, 3 column blocks
+    nbytes = {_lib.W_BF16: cols * 2, _lib.W_INT4: cols // 2}.get(fmt, cols)
+    raw = torch.randint(0, 256, (out, nbytes), generator=g, dtype=torch.uint8)
+    dt = {_lib.W_BF16: torch.bfloat16, _lib.W_INT8: torch.int8}.get(fmt, torch.uint8)
+    q = raw.view(dt)
+    b = quant.block_matrix(q, fmt)
+    assert b.shape == q.shape and b.dtype == q.dtype
+    ub = b.contiguous().view(torch.uint8).flatten()
+    for n in range(out):
+        for byte in range(nbytes):
+            ob, r = divmod(n, 16)
+            if fmt == _lib.W_BF16:
+                col, half = divmod(byte, 2)
+                kb, kk = divmod(col, 64)
+                gg, c = divmod(kk, 16)
+                h, j = divmod(c, 8)
+                off = (ob * (cols // 64) + kb) * 2048 + h * 1024 + (16 * gg + r) * 16 + 2 * j + half
+            else:
+                piece = 8 if fmt == _lib.W_INT4 else 16
+                kb, kk = divmod(byte, 4 * piece)
+                gg, c = divmod(kk, piece)
+                off = (ob * (cols // 64) + kb) * 64 * piece + (16 * gg + r) * piece + c
+            assert int(ub[off]) == int(raw[n, byte])
+    assert torch.equal(quant.unblock_matrix(b, fmt).view(torch.uint8), raw)
+    st = torch.stack([q, q.flip(0)])
+    bs = quant.block_matrix(st, fmt)
+    assert torch.equal(bs[0].view(torch.uint8), b.view(torch.uint8))
+    assert torch.equal(quant.unblock_matrix(bs, fmt).view(torch.uint8), st.view(torch.uint8))
+    f = torch.randn(16, 64, generator=g)
+    assert quant.block_matrix(f, _lib.W_F32) is f          # fp32 stays row-major
+
