@@ -43,6 +43,19 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));  // staging registers (plain vector)
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+// Weight loads of the streaming GEMMs: every expert weight byte is read by exactly one
+// work-group, so the loads are non-temporal — they do not push the activation rows, which
+// every work-group of a tile reads again, out of L2.
+__device__ __forceinline__ uint4 nt_load16(const char* p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint2 nt_load8(const char* p) {
+    const u32x2 v = __builtin_nontemporal_load((const u32x2*)p);
+    return make_uint2(v.x, v.y);
+}
 
 enum Epi { EPI_F32 = 0, EPI_SWIGLU = 1, EPI_DOWN = 2 };
 
@@ -127,8 +140,8 @@ struct BLoad<YVMOE_W_BF16> {
                lane * 16;
     }
     static __device__ __forceinline__ void load_blk(Raw& r, const char* p, int ks) {
-        r.u[0] = *(const uint4*)(p + (size_t)ks * BLK);
-        r.u[1] = *(const uint4*)(p + (size_t)ks * BLK + 1024);
+        r.u[0] = nt_load16(p + (size_t)ks * BLK);
+        r.u[1] = nt_load16(p + (size_t)ks * BLK + 1024);
     }
     static __device__ __forceinline__ void cvt(const Raw& r, float, Frag16& f) { f = r; }
 };
@@ -149,7 +162,7 @@ struct BLoad<YVMOE_W_INT8> {
         return (const char*)base + e_off + ((long long)(n >> 4) * (K / 64) + kbeg / 64) * BLK + lane * 16;
     }
     static __device__ __forceinline__ void load_blk(Raw& r, const char* p, int ks) {
-        r = *(const uint4*)(p + (size_t)ks * BLK);
+        r = nt_load16(p + (size_t)ks * BLK);
     }
     static __device__ __forceinline__ void cvt(const Raw& r, float s, Frag16& f) {
         const unsigned w[4] = {r.x, r.y, r.z, r.w};
@@ -185,7 +198,7 @@ struct BLoad<YVMOE_W_INT4> {
         return (const char*)base + e_off / 2 + ((long long)(n >> 4) * (K / 64) + kbeg / 64) * BLK + lane * 8;
     }
     static __device__ __forceinline__ void load_blk(Raw& r, const char* p, int ks) {
-        r = *(const uint2*)(p + (size_t)ks * BLK);
+        r = nt_load8(p + (size_t)ks * BLK);
     }
     static __device__ __forceinline__ void cvt(const Raw& r, float s, Frag16& f) {
         const unsigned w[2] = {r.x, r.y};
@@ -221,7 +234,7 @@ struct BLoad<YVMOE_W_FP8> {
         return (const char*)base + e_off + ((long long)(n >> 4) * (K / 64) + kbeg / 64) * BLK + lane * 16;
     }
     static __device__ __forceinline__ void load_blk(Raw& r, const char* p, int ks) {
-        r = *(const uint4*)(p + (size_t)ks * BLK);
+        r = nt_load16(p + (size_t)ks * BLK);
     }
     static __device__ __forceinline__ void cvt(const Raw& r, float s, Frag16& f) {
         const unsigned w[4] = {r.x, r.y, r.z, r.w};
