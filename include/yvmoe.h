@@ -114,8 +114,9 @@ typedef struct {
  * Router state of YvStableMoEGate (model/moe/gate.py:895-1028).
  *   w_router : activations bf16 -> bf16 [Ep + 192][H] = [gate.weight padded to Ep rows;
  *              W1 hi; W1 mid; W1 lo], where W1 = complexity_predictor[0].weight [64][H]
- *              split into three bf16 terms whose sum is W1 exactly;
- *              activations fp32 -> fp32 [Ep + 64][H] = [gate.weight padded; W1].
+ *              split into three bf16 terms whose sum is W1 exactly, stored in the
+ *              16 x 64 block order of yvmoe_expert_weights (BF16);
+ *              activations fp32 -> fp32 [Ep + 64][H] = [gate.weight padded; W1], row-major.
  *              Ep = E rounded up to a multiple of 16 (padding rows are zero).
  *   b1 [64], w2 [64], b2 [1] : the rest of complexity_predictor (fp32).
  *   bias [E] or NULL : added to the logits before the softmax — expert_bias in
@@ -219,14 +220,15 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
  *           rows [0, dg_dim) hicl_dg_encoder.dg_proj.weight; then Rh = round_up(4E + D, 256)
  *           head rows: gate.weight, got_cluster_proj.weight, gate_k.weight, gate_v.weight
  *           (E rows each), input_encoder.0.weight (D rows), zero rows.
- *           P = dg_dim + Rh with the HiCL head, Rh without;
+ *           P = dg_dim + Rh with the HiCL head, Rh without; bf16: in the 16 x 64 block
+ *           order of yvmoe_expert_weights (BF16), fp32: row-major;
  *   dg_bias [dg_dim];
  *   prototypes_t [dg_dim][E] = hicl_prototypesᵀ;
  *   eo_mat [D][E] = input_encoder.2.weightᵀ · expert_capability_encoder(expert_embeddings)ᵀ:
  *           the Expert-Oriented head's two linear maps after the SiLU folded into one constant
  *           of the weights (gate.py:362-364);
  *   modal_affinity [E][n_modalities] expert_modal_affinity; expert_bias [E] or NULL.
- * All fp32 except w_heads / w_dg. heads: the auxiliary heads computed (YVMOE_HEAD_*; the
+ * All fp32 except w_proj. heads: the auxiliary heads computed (YVMOE_HEAD_*; the
  * reference skips pruned ones, gate.py:263-276). temperature is the effective one of
  * _safe_temperature (gate.py:297-308), soft_eps = YvNumericalGuard.get_eps(dtype),
  * capacity_loss = 0.005 · Σ relu(usage - limit)² from the usage buffers (gate.py:586-591).

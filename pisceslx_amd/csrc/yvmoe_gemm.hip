@@ -45,9 +45,10 @@ typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));  // staging registers (plain vector)
 typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 
-// Weight loads of the streaming GEMMs: every expert weight byte is read by exactly one
-// work-group, so the loads are non-temporal — they do not push the activation rows, which
-// every work-group of a tile reads again, out of L2.
+// Weight loads of the streaming kernel: at decode sizes every weight byte is read by one
+// work-group (a few for the shared experts, right after each other), so the loads are
+// non-temporal — they do not push the activation rows, which every work-group of a tile
+// reads again, out of L2.
 __device__ __forceinline__ uint4 nt_load16(const char* p) {
     const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
     return make_uint4(v.x, v.y, v.z, v.w);
@@ -115,12 +116,13 @@ union Frag16 {  // 16 bf16 = two MFMA operands
 template <int WF>
 struct BLoad;
 
-// Expert matrices are stored in 16-row x 64-column blocks (pisceslx_amd/quant.py
-// block_matrix): lane l = 16 g + r of a 16-column group reads piece (g, r) of each block, a
-// contiguous 16 bytes per lane (8 for int4; bf16 pieces are split in two halves 1 KB apart).
-// bptr() is the lane's address of its piece in the first block of column group n / 16 from
-// K offset kbeg; load_blk() reads the piece of the ks-th 64-wide block after it. Dense
-// weights (router, gate projections) stay row-major and use ptr() / load().
+// Weight operands (expert matrices, the router and gate projections; all but fp32) are stored
+// in 16-row x 64-column blocks (pisceslx_amd/quant.py block_matrix): lane l = 16 g + r of a
+// 16-column group reads piece (g, r) of each block, a contiguous 16 bytes per lane (8 for
+// int4; bf16 pieces are split in two halves 1 KB apart). bptr() is the lane's address of its
+// piece in the first block of column group n / 16 from K offset kbeg; load_blk() reads the
+// piece of the ks-th 64-wide block after it (load_blk_nt() non-temporally); ptr() / load()
+// address the row-major order.
 template <>
 struct BLoad<YVMOE_W_BF16> {
     typedef Frag16 Raw;
@@ -140,6 +142,10 @@ struct BLoad<YVMOE_W_BF16> {
                lane * 16;
     }
     static __device__ __forceinline__ void load_blk(Raw& r, const char* p, int ks) {
+        r.u[0] = *(const uint4*)(p + (size_t)ks * BLK);
+        r.u[1] = *(const uint4*)(p + (size_t)ks * BLK + 1024);
+    }
+    static __device__ __forceinline__ void load_blk_nt(Raw& r, const char* p, int ks) {
         r.u[0] = nt_load16(p + (size_t)ks * BLK);
         r.u[1] = nt_load16(p + (size_t)ks * BLK + 1024);
     }
@@ -162,6 +168,9 @@ struct BLoad<YVMOE_W_INT8> {
         return (const char*)base + e_off + ((long long)(n >> 4) * (K / 64) + kbeg / 64) * BLK + lane * 16;
     }
     static __device__ __forceinline__ void load_blk(Raw& r, const char* p, int ks) {
+        r = *(const uint4*)(p + (size_t)ks * BLK);
+    }
+    static __device__ __forceinline__ void load_blk_nt(Raw& r, const char* p, int ks) {
         r = nt_load16(p + (size_t)ks * BLK);
     }
     static __device__ __forceinline__ void cvt(const Raw& r, float s, Frag16& f) {
@@ -198,6 +207,9 @@ struct BLoad<YVMOE_W_INT4> {
         return (const char*)base + e_off / 2 + ((long long)(n >> 4) * (K / 64) + kbeg / 64) * BLK + lane * 8;
     }
     static __device__ __forceinline__ void load_blk(Raw& r, const char* p, int ks) {
+        r = *(const uint2*)(p + (size_t)ks * BLK);
+    }
+    static __device__ __forceinline__ void load_blk_nt(Raw& r, const char* p, int ks) {
         r = nt_load8(p + (size_t)ks * BLK);
     }
     static __device__ __forceinline__ void cvt(const Raw& r, float s, Frag16& f) {
@@ -234,6 +246,9 @@ struct BLoad<YVMOE_W_FP8> {
         return (const char*)base + e_off + ((long long)(n >> 4) * (K / 64) + kbeg / 64) * BLK + lane * 16;
     }
     static __device__ __forceinline__ void load_blk(Raw& r, const char* p, int ks) {
+        r = *(const uint4*)(p + (size_t)ks * BLK);
+    }
+    static __device__ __forceinline__ void load_blk_nt(Raw& r, const char* p, int ks) {
         r = nt_load16(p + (size_t)ks * BLK);
     }
     static __device__ __forceinline__ void cvt(const Raw& r, float s, Frag16& f) {
@@ -287,7 +302,7 @@ struct NMat {
 template <int WF, int EPI, int NCB, int MAXRB, int RB = 4, int RA = 2>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
     constexpr int NM = NMat<EPI>::value;
-    constexpr bool BLKD = EPI != EPI_F32;  // expert matrices are blocked, dense ones row-major
+    constexpr bool BLKD = true;  // bf16-activation kernel: weights are bf16/int8/int4/fp8, blocked
     constexpr bool GROUPED = (WF == YVMOE_W_INT4 || WF == YVMOE_W_FP8);
     static_assert(RB % RA == 0, "A ring depth must divide the B ring depth");
     constexpr int R = RB;
@@ -472,7 +487,7 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
                                             uint4 (&As)[2][16 * MAXRB * (U * 8 + 1)]) {
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
     constexpr bool GROUPED = (WF == YVMOE_W_INT4 || WF == YVMOE_W_FP8);
-    constexpr bool BLKD = EPI != EPI_F32;  // expert matrices are blocked, dense ones row-major
+    constexpr bool BLKD = WF != YVMOE_W_F32;  // all weight operands but fp32 are blocked
     constexpr int ROWS = 16 * MAXRB;
     constexpr int ROW_U4 = U * 8 + 1;            // uint4 per staged row (U*64 bf16 + pad)
     constexpr int CHUNK_U4 = ROWS * U * 8;       // uint4 of one chunk
@@ -564,7 +579,7 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const int ks = min(ks0 + u, nks - 1);
-                    if constexpr (BLKD) BL::load_blk(bw[b][u], bptr[b], ks);
+                    if constexpr (BLKD) BL::load_blk_nt(bw[b][u], bptr[b], ks);
                     else BL::load(bw[b][u], bptr[b], ks * 64);
                     if constexpr (GROUPED) sg[b][u] = b_scale<WF>(S, s_off, n[b], p.K, kbeg + ks * 64);
                     else sg[b][u] = scl[b];
@@ -749,7 +764,7 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     typedef TileCfg<WF> C;
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
     constexpr bool GROUPED = WF == YVMOE_W_FP8;
-    constexpr bool BLKD = EPI != EPI_F32;                              // blocked expert weights
+    constexpr bool BLKD = true;                                        // blocked weights
     constexpr long long B_CHUNK = BLKD ? 1024LL * C::EB : TBK * C::EB;  // bytes per 64-wide step
     static_assert(WF == YVMOE_W_INT8 || WF == YVMOE_W_FP8 || WF == YVMOE_W_BF16,
                   "tiled form covers 1- and 2-byte weight formats");

@@ -27,7 +27,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from . import functional as yvf
-from .quant import pack_router
+from .quant import block_matrix, pack_router
 
 
 class YvStableMoEGate(nn.Module):
@@ -318,6 +318,8 @@ class YvMoEGate(nn.Module):
             w_proj[dg + 2 * E:dg + 3 * E] = self.gate_k.weight
             w_proj[dg + 3 * E:dg + 4 * E] = self.gate_v.weight
             w_proj[dg + 4 * E:dg + 4 * E + D] = self.input_encoder[0].weight
+            if act == _lib.ACT_BF16:
+                w_proj = block_matrix(w_proj, _lib.W_BF16)  # the GEMM kernels' blocked order
             dg_bias = enc.dg_bias.detach().float().contiguous()
             proto_t = self.hicl_prototypes.detach().float().t().contiguous()
             # Expert-Oriented: silu(enc0 x) · enc2ᵀ · eeᵀ with ee = cap2(silu(cap0(emb))), a

@@ -296,8 +296,8 @@ def pack_router(gate_weight: torch.Tensor, pred_w1: Optional[torch.Tensor], act:
     """Router GEMM operand: [gate.weight padded to Ep rows; predictor W1 terms] ([out][H]).
 
     bf16 activations: bf16 [Ep + 192][H] with W1 split into three bf16 terms so the bf16
-    MFMA reproduces the fp32 predictor (complexity_predictor is fp32, gate.py:930-936).
-    fp32 activations: fp32 [Ep + 64][H].
+    MFMA reproduces the fp32 predictor (complexity_predictor is fp32, gate.py:930-936), in
+    the blocked order of :func:`block_matrix`. fp32 activations: fp32 [Ep + 64][H] row-major.
     """
     E, H = gate_weight.shape
     Ep = (E + 15) // 16 * 16
@@ -308,7 +308,7 @@ def pack_router(gate_weight: torch.Tensor, pred_w1: Optional[torch.Tensor], act:
         g = torch.zeros(Ep, H, dtype=torch.bfloat16, device=dev)
         g[:E] = gate_weight.to(torch.bfloat16)
         hi, mid, lo = split_bf16x3(pred_w1.to(dev))
-        return torch.cat([g, hi, mid, lo], dim=0).contiguous()
+        return block_matrix(torch.cat([g, hi, mid, lo], dim=0).contiguous(), _lib.W_BF16)
     g = torch.zeros(Ep, H, dtype=torch.float32, device=dev)
     g[:E] = gate_weight.float()
     return torch.cat([g, pred_w1.float().to(dev)], dim=0).contiguous()

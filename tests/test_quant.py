@@ -73,7 +73,9 @@ def test_router_split_is_exact_to_one_ulp():
     ulp = torch.abs(w1.double()) * 2.0 ** -23
     assert ((recon - w1.double()).abs() <= ulp + 1e-45).all()
     wr = quant.pack_router(torch.randn(10, 512, generator=g).to(torch.bfloat16), w1, _lib.ACT_BF16)
-    assert wr.shape == (16 + 192, 512) and (wr[10:16] == 0).all()
+    assert wr.shape == (16 + 192, 512)
+    wr = quant.unblock_matrix(wr, _lib.W_BF16)                 # stored in the blocked order
+    assert (wr[10:16] == 0).all() and torch.equal(wr[16:80], hi) and torch.equal(wr[144:], lo)
     wr32 = quant.pack_router(torch.randn(10, 512, generator=g), w1, _lib.ACT_F32)
     assert wr32.shape == (16 + 64, 512) and torch.equal(wr32[16:], w1)
 
