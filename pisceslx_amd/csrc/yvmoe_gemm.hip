@@ -127,15 +127,6 @@ template <>
 struct BLoad<YVMOE_W_BF16> {
     typedef Frag16 Raw;
     static constexpr int BLK = 2048;
-    static __device__ __forceinline__ const char* ptr(const void* base, long long e_off, int n,
-                                                      int K, int kl) {
-        return (const char*)base + (e_off + (long long)n * K + kl) * 2;
-    }
-    static __device__ __forceinline__ void load(Raw& r, const char* p, int k0) {
-        const uint4* q = (const uint4*)(p + (size_t)k0 * 2);
-        r.u[0] = q[0];
-        r.u[1] = q[1];
-    }
     static __device__ __forceinline__ const char* bptr(const void* base, long long e_off, int n,
                                                        int K, int kbeg, int lane) {
         return (const char*)base + e_off * 2 + ((long long)(n >> 4) * (K / 64) + kbeg / 64) * BLK +
@@ -156,13 +147,6 @@ template <>
 struct BLoad<YVMOE_W_INT8> {
     typedef uint4 Raw;
     static constexpr int BLK = 1024;
-    static __device__ __forceinline__ const char* ptr(const void* base, long long e_off, int n,
-                                                      int K, int kl) {
-        return (const char*)base + (e_off + (long long)n * K + kl);
-    }
-    static __device__ __forceinline__ void load(Raw& r, const char* p, int k0) {
-        r = *(const uint4*)(p + k0);
-    }
     static __device__ __forceinline__ const char* bptr(const void* base, long long e_off, int n,
                                                        int K, int kbeg, int lane) {
         return (const char*)base + e_off + ((long long)(n >> 4) * (K / 64) + kbeg / 64) * BLK + lane * 16;
@@ -194,14 +178,6 @@ template <>
 struct BLoad<YVMOE_W_INT4> {
     typedef uint2 Raw;
     static constexpr int BLK = 512;
-    static __device__ __forceinline__ const char* ptr(const void* base, long long e_off, int n,
-                                                      int K, int kl) {
-        // e_off, n * K and kl count int4 elements (all even): two per byte
-        return (const char*)base + (e_off + (long long)n * K + kl) / 2;
-    }
-    static __device__ __forceinline__ void load(Raw& r, const char* p, int k0) {
-        r = *(const uint2*)(p + k0 / 2);
-    }
     static __device__ __forceinline__ const char* bptr(const void* base, long long e_off, int n,
                                                        int K, int kbeg, int lane) {
         return (const char*)base + e_off / 2 + ((long long)(n >> 4) * (K / 64) + kbeg / 64) * BLK + lane * 8;
@@ -234,13 +210,6 @@ template <>
 struct BLoad<YVMOE_W_FP8> {
     typedef uint4 Raw;
     static constexpr int BLK = 1024;
-    static __device__ __forceinline__ const char* ptr(const void* base, long long e_off, int n,
-                                                      int K, int kl) {
-        return (const char*)base + (e_off + (long long)n * K + kl);
-    }
-    static __device__ __forceinline__ void load(Raw& r, const char* p, int k0) {
-        r = *(const uint4*)(p + k0);
-    }
     static __device__ __forceinline__ const char* bptr(const void* base, long long e_off, int n,
                                                        int K, int kbeg, int lane) {
         return (const char*)base + e_off + ((long long)(n >> 4) * (K / 64) + kbeg / 64) * BLK + lane * 16;
@@ -302,7 +271,6 @@ struct NMat {
 template <int WF, int EPI, int NCB, int MAXRB, int RB = 4, int RA = 2>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
     constexpr int NM = NMat<EPI>::value;
-    constexpr bool BLKD = true;  // bf16-activation kernel: weights are bf16/int8/int4/fp8, blocked
     constexpr bool GROUPED = (WF == YVMOE_W_INT4 || WF == YVMOE_W_FP8);
     static_assert(RB % RA == 0, "A ring depth must divide the B ring depth");
     constexpr int R = RB;
@@ -343,13 +311,8 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
 #pragma unroll
     for (int cb = 0; cb < NCB; ++cb) {
         ncol[cb] = col0 + cb * 16 + (lane & 15);
-        if constexpr (BLKD) {
-            bptr[0][cb] = BL::bptr(p.B0, e_off, ncol[cb], p.K, kbeg, lane);
-            if constexpr (NM == 2) bptr[NM - 1][cb] = BL::bptr(p.B1, e_off, ncol[cb], p.K, kbeg, lane);
-        } else {
-            bptr[0][cb] = BL::ptr(p.B0, e_off, ncol[cb], p.K, kbeg + kl);
-            if constexpr (NM == 2) bptr[NM - 1][cb] = BL::ptr(p.B1, e_off, ncol[cb], p.K, kbeg + kl);
-        }
+        bptr[0][cb] = BL::bptr(p.B0, e_off, ncol[cb], p.K, kbeg, lane);
+        if constexpr (NM == 2) bptr[NM - 1][cb] = BL::bptr(p.B1, e_off, ncol[cb], p.K, kbeg, lane);
     }
 
     f32x4 acc[NM][NCB][MAXRB];
@@ -375,8 +338,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
         for (int m = 0; m < NM; ++m)
 #pragma unroll
             for (int cb = 0; cb < NCB; ++cb) {
-                if constexpr (BLKD) BL::load_blk(dst[m][cb], bptr[m][cb], slot_ks);
-                else BL::load(dst[m][cb], bptr[m][cb], k0);
+                BL::load_blk(dst[m][cb], bptr[m][cb], slot_ks);
                 if constexpr (GROUPED)
                     sdst[m][cb] = b_scale<WF>(sptr[m], s_off, ncol[cb], p.K, kbeg + k0);
             }
@@ -487,7 +449,6 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
                                             uint4 (&As)[2][16 * MAXRB * (U * 8 + 1)]) {
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
     constexpr bool GROUPED = (WF == YVMOE_W_INT4 || WF == YVMOE_W_FP8);
-    constexpr bool BLKD = WF != YVMOE_W_F32;  // all weight operands but fp32 are blocked
     constexpr int ROWS = 16 * MAXRB;
     constexpr int ROW_U4 = U * 8 + 1;            // uint4 per staged row (U*64 bf16 + pad)
     constexpr int CHUNK_U4 = ROWS * U * 8;       // uint4 of one chunk
@@ -508,7 +469,6 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
     const int mat = SWIGLU ? (wave & 1) : 0;  // 0: gate (or down), 1: up
     // first column of block b of this wavefront
     const int colw = SWIGLU ? (cgroup * 2 + (wave >> 1)) * 16 * NB : (cgroup * 4 + wave) * 16 * NB;
-    const int kl = (lane >> 4) * 16;
     // K range of split kz (EPI_F32 writes split kz's partial sums at kz * split_stride)
     const int kbeg = kz * p.kchunk;
     const int kend = min(p.K, kbeg + p.kchunk);
@@ -552,8 +512,7 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
         const int c0 = colw + b * 16;
         active[b] = c0 < p.ncols;  // blocks past the last column still stage and sync
         n[b] = min(c0, p.ncols - 16) + (lane & 15);
-        if constexpr (BLKD) bptr[b] = BL::bptr(mat ? p.B1 : p.B0, e_off, n[b], p.K, kbeg, lane);
-        else bptr[b] = BL::ptr(mat ? p.B1 : p.B0, e_off, n[b], p.K, kbeg + kl);
+        bptr[b] = BL::bptr(mat ? p.B1 : p.B0, e_off, n[b], p.K, kbeg, lane);
         scl[b] = b_scale<WF>(S, s_off, n[b], p.K, 0);
     }
 
@@ -579,8 +538,7 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
                     const int ks = min(ks0 + u, nks - 1);
-                    if constexpr (BLKD) BL::load_blk_nt(bw[b][u], bptr[b], ks);
-                    else BL::load(bw[b][u], bptr[b], ks * 64);
+                    BL::load_blk_nt(bw[b][u], bptr[b], ks);
                     if constexpr (GROUPED) sg[b][u] = b_scale<WF>(S, s_off, n[b], p.K, kbeg + ks * 64);
                     else sg[b][u] = scl[b];
                 }
@@ -714,12 +672,12 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(GemmParams p, int ngro
 // up of columns 16 w .. 16 w + 15 and finishes SwiGLU in registers.
 //
 // Each lane's MFMA operands cover 16 consecutive k of the chunk (k group l / 16), split over
-// the two MFMAs of a chunk in the same order for both operands. LDS layouts are swizzled in
-// 16-byte chunks so the fragment reads run without bank conflicts (measured): activation
-// rows (128 B) put chunk c of row r at c ^ (r & 7) ^ ((r >> 3) & 1), 1-byte weight rows
-// (64 B) put chunk c at c ^ ((r >> 1) & 3). The writes follow from the lane order of the
-// direct loads: lane L of a 1 KB block fetches the logical chunk that the swizzle places at
-// position L.
+// the two MFMAs of a chunk in the same order for both operands. Activation rows (128 B) are
+// swizzled in 16-byte chunks so the fragment reads run without bank conflicts (measured):
+// chunk c of row r sits at c ^ (r & 7) ^ ((r >> 3) & 1), and lane L of a 1 KB direct load
+// fetches the logical chunk that the swizzle places at position L. Weight blocks arrive in
+// the order the fragment reads want (lane l reads bytes 16 l of its row block's 1 KB, and
+// of the second 1 KB for bf16): contiguous, conflict-free, no swizzle.
 constexpr int TBM = 256, TBN = 256, TBK = 64;
 constexpr int TTHREADS = 1024;
 
@@ -735,9 +693,6 @@ __device__ __forceinline__ void dma16(const void* src, void* dst) {
 
 __device__ __forceinline__ int swz_a(int r, int c) {  // bytes, 128-byte rows
     return r * 128 + ((c ^ (r & 7) ^ ((r >> 3) & 1)) << 4);
-}
-__device__ __forceinline__ int swz_b(int r, int c) {  // bytes, 64-byte rows
-    return r * 64 + ((c ^ ((r >> 1) & 3)) << 4);
 }
 
 // s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt in bits 3:0 and
@@ -764,8 +719,7 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     typedef TileCfg<WF> C;
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
     constexpr bool GROUPED = WF == YVMOE_W_FP8;
-    constexpr bool BLKD = true;                                        // blocked weights
-    constexpr long long B_CHUNK = BLKD ? 1024LL * C::EB : TBK * C::EB;  // bytes per 64-wide step
+    constexpr long long B_CHUNK = 1024LL * C::EB;  // bytes of a weight block (64-wide K step)
     static_assert(WF == YVMOE_W_INT8 || WF == YVMOE_W_FP8 || WF == YVMOE_W_BF16,
                   "tiled form covers 1- and 2-byte weight formats");
     __shared__ __attribute__((aligned(1024))) unsigned char lds_a[C::NST][C::A_BYTES];
@@ -806,32 +760,17 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
         const int gr = (row0 + r < seg_end) ? row0 + r : row0;
         a_src[j] = (const char*)p.A + ((long long)map_row(p, gr) * p.lda + lc * 8) * 2;
     }
-    // weight blocks: expert matrices are stored in 16-row x 64-column blocks (1 KB per 1-byte
-    // block, two 1 KB halves per bf16 block) that land in LDS as stored, block after block;
-    // dense weights (EPI_F32) are row-major and land swizzled like the activations
+    // weight blocks: 16-row x 64-column blocks (1 KB per 1-byte block, two 1 KB halves per
+    // bf16 block) land in LDS as stored, block after block
     const char* b_src[C::B_DMA];
 #pragma unroll
     for (int j = 0; j < C::B_DMA; ++j) {
         const int blk = wave * C::B_DMA + j;
-        if constexpr (BLKD) {
-            const int r16 = (blk / C::EB) * 16, half = blk % C::EB;
-            const void* B = (SWIGLU && r16 >= TBN / 2) ? p.B1 : p.B0;
-            const int nb16 = SWIGLU ? n0 + (r16 & (TBN / 2 - 1)) : n0 + r16;
-            b_src[j] = (const char*)B + e_off * C::EB + (long long)(nb16 >> 4) * (p.K / 64) * B_CHUNK +
-                       half * 1024 + lane * 16;
-        } else {
-            int r, lc;
-            if constexpr (C::EB == 1) {
-                r = blk * 16 + lane / 4;
-                lc = (lane % 4) ^ ((r >> 1) & 3);
-            } else {
-                r = blk * 8 + lane / 8;
-                lc = (lane % 8) ^ (r & 7) ^ ((r >> 3) & 1);
-            }
-            const void* B = (SWIGLU && r >= TBN / 2) ? p.B1 : p.B0;
-            const int n = SWIGLU ? n0 + (r & (TBN / 2 - 1)) : n0 + r;
-            b_src[j] = (const char*)B + (e_off + (long long)n * p.K) * C::EB + lc * 16;
-        }
+        const int r16 = (blk / C::EB) * 16, half = blk % C::EB;
+        const void* B = (SWIGLU && r16 >= TBN / 2) ? p.B1 : p.B0;
+        const int nb16 = SWIGLU ? n0 + (r16 & (TBN / 2 - 1)) : n0 + r16;
+        b_src[j] = (const char*)B + e_off * C::EB + (long long)(nb16 >> 4) * (p.K / 64) * B_CHUNK +
+                   half * 1024 + lane * 16;
     }
 
     // this lane's weight rows in the tile (fragment column l % 16 of each 16-row block)
@@ -871,17 +810,9 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     const int a_rd0 = swz_a(wr * 128 + (lane & 15), 2 * g), a_rd1 = swz_a(wr * 128 + (lane & 15), 2 * g + 1);
     int b_rd0[2], b_rd1[2];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        if constexpr (BLKD) {  // piece (g, r) of the row's block: lane * 16 (second half + 1 KB)
-            b_rd0[nb] = (brow[nb] >> 4) * 1024 * C::EB + lane * 16;
-            b_rd1[nb] = b_rd0[nb] + 1024;
-        } else if constexpr (C::EB == 1) {
-            b_rd0[nb] = swz_b(brow[nb], g);
-            b_rd1[nb] = 0;
-        } else {
-            b_rd0[nb] = swz_a(brow[nb], 2 * g);
-            b_rd1[nb] = swz_a(brow[nb], 2 * g + 1);
-        }
+    for (int nb = 0; nb < 2; ++nb) {  // piece (g, r) of the row's block: lane * 16 (+ 1 KB)
+        b_rd0[nb] = (brow[nb] >> 4) * 1024 * C::EB + lane * 16;
+        b_rd1[nb] = b_rd0[nb] + 1024;
     }
 
     // The direct loads are issued from inline assembly: the compiler's own form of them makes
