@@ -690,6 +690,11 @@ __device__ __forceinline__ void dma16(const void* src, void* dst) {
     const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_ptr_t)dst);
     asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(src) : "memory", "m0");
 }
+// The same with 4 bytes per lane (256 B per wavefront at dst + 4 L).
+__device__ __forceinline__ void dma4(const void* src, void* dst) {
+    const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_ptr_t)dst);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" : : "s"(m0), "v"(src) : "memory", "m0");
+}
 
 __device__ __forceinline__ int swz_a(int r, int c) {  // bytes, 128-byte rows
     return r * 128 + ((c ^ (r & 7) ^ ((r >> 3) & 1)) << 4);
@@ -701,13 +706,17 @@ constexpr int vmcnt_only(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 
 
 template <int WF>
 struct TileCfg {
-    static constexpr int EB = (WF == YVMOE_W_BF16) ? 2 : 1;  // bytes per weight
+    static constexpr bool I4 = WF == YVMOE_W_INT4;
+    static constexpr int EB = (WF == YVMOE_W_BF16) ? 2 : 1;  // bytes per weight (int4: half)
     static constexpr int NST = (EB == 2) ? 2 : 3;             // LDS stages (160 KB of LDS)
     static constexpr int A_BYTES = TBM * TBK * 2;
-    static constexpr int B_BYTES = TBN * TBK * EB;
+    static constexpr int B_BYTES = I4 ? TBN * TBK / 2 : TBN * TBK * EB;
+    static constexpr int B_BLK = I4 ? 512 : 1024 * EB;  // bytes of a 16-row weight block
     static constexpr int A_DMA = A_BYTES / 1024 / (TTHREADS / 64);  // 1 KB direct loads per wavefront
-    static constexpr int B_DMA = B_BYTES / 1024 / (TTHREADS / 64);
+    // weight direct loads per wavefront: 1 KB each (int4: 256 B dword loads, two per block)
+    static constexpr int B_DMA = I4 ? 2 : B_BYTES / 1024 / (TTHREADS / 64);
     static constexpr int NPW = A_DMA + B_DMA;
+    static constexpr int S4 = I4 ? TBN * 64 : 1;  // int4: the tile's group scales, K <= 8192
 };
 
 // Work items are (tile, column block) pairs, column block fastest, so the work-groups that
@@ -719,12 +728,11 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     typedef TileCfg<WF> C;
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
     constexpr bool GROUPED = WF == YVMOE_W_FP8;
-    constexpr long long B_CHUNK = 1024LL * C::EB;  // bytes of a weight block (64-wide K step)
-    static_assert(WF == YVMOE_W_INT8 || WF == YVMOE_W_FP8 || WF == YVMOE_W_BF16,
-                  "tiled form covers 1- and 2-byte weight formats");
+    constexpr long long B_CHUNK = C::B_BLK;  // bytes of a weight block (64-wide K step)
     __shared__ __attribute__((aligned(1024))) unsigned char lds_a[C::NST][C::A_BYTES];
     __shared__ __attribute__((aligned(1024))) unsigned char lds_b[C::NST][C::B_BYTES];
     __shared__ float lds_s[2][64];  // fp8: block scales of the tile's two 128-row weight blocks
+    __shared__ unsigned short lds_s4[C::S4];  // int4: bf16 scale of tile row r, group q at r * K/128 + q
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
@@ -762,15 +770,21 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     }
     // weight blocks: 16-row x 64-column blocks (1 KB per 1-byte block, two 1 KB halves per
     // bf16 block) land in LDS as stored, block after block
+    // (int4: 512-byte blocks, each loaded as two 256-byte halves by one wavefront)
     const char* b_src[C::B_DMA];
+    int b_dst[C::B_DMA];
 #pragma unroll
     for (int j = 0; j < C::B_DMA; ++j) {
         const int blk = wave * C::B_DMA + j;
-        const int r16 = (blk / C::EB) * 16, half = blk % C::EB;
+        const int rb = C::I4 ? wave : blk / C::EB;           // 16-row block of the tile
+        const int half = C::I4 ? j : blk % C::EB;
+        const int r16 = rb * 16;
         const void* B = (SWIGLU && r16 >= TBN / 2) ? p.B1 : p.B0;
         const int nb16 = SWIGLU ? n0 + (r16 & (TBN / 2 - 1)) : n0 + r16;
-        b_src[j] = (const char*)B + e_off * C::EB + (long long)(nb16 >> 4) * (p.K / 64) * B_CHUNK +
-                   half * 1024 + lane * 16;
+        const long long e_bytes = C::I4 ? e_off / 2 : e_off * C::EB;
+        b_src[j] = (const char*)B + e_bytes + (long long)(nb16 >> 4) * (p.K / 64) * B_CHUNK +
+                   (C::I4 ? half * 256 + lane * 4 : half * 1024 + lane * 16);
+        b_dst[j] = C::I4 ? rb * 512 + half * 256 : blk * 1024;
     }
 
     // this lane's weight rows in the tile (fragment column l % 16 of each 16-row block)
@@ -787,6 +801,17 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
             const void* S = (SWIGLU && r >= TBN / 2) ? p.S1 : p.S0;
             cs[nb] = b_scale<WF>(S, s_off, SWIGLU ? n0 + (r & (TBN / 2 - 1)) : n0 + r, p.K, 0);
         }
+    }
+    if constexpr (C::I4) {
+        // the tile's group scales into LDS before any direct load is in flight
+        const int kg = p.K / 128;
+        for (int i = t; i < TBN * kg; i += TTHREADS) {
+            const int r = i / kg, q = i % kg;
+            const void* S = (SWIGLU && r >= TBN / 2) ? p.S1 : p.S0;
+            const int n = SWIGLU ? n0 + (r & (TBN / 2 - 1)) : n0 + r;
+            lds_s4[i] = ((const unsigned short*)S)[s_off + (long long)n * kg + q];
+        }
+        __syncthreads();
     }
     if constexpr (GROUPED) {
         const int kb = p.K / 128;
@@ -811,7 +836,7 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     int b_rd0[2], b_rd1[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {  // piece (g, r) of the row's block: lane * 16 (+ 1 KB)
-        b_rd0[nb] = (brow[nb] >> 4) * 1024 * C::EB + lane * 16;
+        b_rd0[nb] = (brow[nb] >> 4) * C::B_BLK + lane * (C::I4 ? 8 : 16);
         b_rd1[nb] = b_rd0[nb] + 1024;
     }
 
@@ -822,8 +847,10 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     do {                                                                                               \
         _Pragma("unroll") for (int j = 0; j < C::A_DMA; ++j)                                           \
             dma16(a_src[j] + (size_t)(CHUNK) * TBK * 2, &lds_a[ST][(wave * C::A_DMA + j) * 1024]);     \
-        _Pragma("unroll") for (int j = 0; j < C::B_DMA; ++j)                                           \
-            dma16(b_src[j] + (size_t)(CHUNK) * B_CHUNK, &lds_b[ST][(wave * C::B_DMA + j) * 1024]);     \
+        _Pragma("unroll") for (int j = 0; j < C::B_DMA; ++j) {                                         \
+            if constexpr (C::I4) dma4(b_src[j] + (size_t)(CHUNK) * B_CHUNK, &lds_b[ST][b_dst[j]]);     \
+            else dma16(b_src[j] + (size_t)(CHUNK) * B_CHUNK, &lds_b[ST][b_dst[j]]);                    \
+        }                                                                                              \
     } while (0)
 
     YV_TILE_ISSUE(0, 0);
@@ -848,7 +875,14 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
         bf16x8 bq[2][2];
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            if constexpr (C::EB == 1) {
+            if constexpr (C::I4) {
+                const u32x2 raw = *(const u32x2*)(Bs + b_rd0[nb]);
+                const float s = bf16_to_f32(lds_s4[brow[nb] * (p.K / 128) + (c * TBK) / 128]);
+                Frag16 f;
+                BLoad<WF>::cvt(make_uint2(raw.x, raw.y), s, f);
+                bq[nb][0] = f.v[0];
+                bq[nb][1] = f.v[1];
+            } else if constexpr (C::EB == 1) {
                 const u32x4 raw = *(const u32x4*)(Bs + b_rd0[nb]);
                 const float s = GROUPED ? lds_s[sblk[nb]][(c * TBK) / 128] : cs[nb];
                 Frag16 f;
@@ -1205,6 +1239,13 @@ int tile_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, c
             case YVMOE_W_BF16: gemm_tile_kernel<YVMOE_W_BF16, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
             case YVMOE_W_INT8: gemm_tile_kernel<YVMOE_W_INT8, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
             case YVMOE_W_FP8: gemm_tile_kernel<YVMOE_W_FP8, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
+            case YVMOE_W_INT4:
+                if (p.K > 8192) {  // the group-scale table in LDS holds K / 128 <= 64 groups
+                    set_error("%s: tiled int4 form needs K <= 8192 (K=%d)", name, p.K);
+                    return YVMOE_ERR_SHAPE;
+                }
+                gemm_tile_kernel<YVMOE_W_INT4, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb);
+                break;
             default: set_error("%s: no tiled form for weight format %d", name, wf); return YVMOE_ERR_DTYPE;
         }
     }
@@ -1358,7 +1399,7 @@ int ffn_tile_rows(int act, int N, int k, int E, int H, int F, int wf) {
     // 256-row LDS-tiled form when experts hold many rows (prefill-like batches)
     const bool tiled = act == YVMOE_ACT_BF16 && N * k >= 64 * E && F % (TBN / 2) == 0 && H % TBN == 0 &&
                        (wf == YVMOE_W_INT8 || wf == YVMOE_W_BF16 ||
-                        (wf == YVMOE_W_FP8 && H <= 8192 && F <= 8192));
+                        ((wf == YVMOE_W_FP8 || wf == YVMOE_W_INT4) && H <= 8192 && F <= 8192));
     if (tiled) return TBM;
     // 16-row tiles (one MFMA row block per wave) when experts hold few rows (decode-like
     // batches), 64-row tiles otherwise

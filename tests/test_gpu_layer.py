@@ -122,6 +122,15 @@ def test_cfg3_full_size_sampled_tokens(cuda, oracle):
     _run_and_check(oracle, w, tokens=tokens)
 
 
+def test_cfg4_full_size_tiled_int4_sampled_tokens(cuda, oracle):
+    """cfg4 at its full size (4344 tokens, N*k >= 64*E): the LDS-tiled form with int4 weights
+    (group scales staged in LDS, 512-byte weight blocks), checked on sampled tokens."""
+    w = make_workload("cfg4", device="cuda")
+    rng = np.random.default_rng(1)
+    tokens = np.sort(rng.choice(w.n_tokens, 64, replace=False))
+    _run_and_check(oracle, w, tokens=tokens)
+
+
 def test_bf16_and_small_shapes(cuda, oracle):
     # unquantized bf16 experts on a small layer, ragged odd lengths
     from pisceslx_amd import _lib
