@@ -26,6 +26,8 @@
 // which leaves the sum unchanged.
 #include <algorithm>
 
+#include <type_traits>
+
 #include "yvmoe_internal.h"
 
 #ifndef YV_NB1
@@ -853,6 +855,10 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
         }                                                                                              \
     } while (0)
 
+    // 16-row blocks of this wavefront's 128 rows that hold rows of the segment: an expert's
+    // last tile skips the MFMAs of the blocks past its end (loads and barriers stay uniform)
+    const int live_mb = min(8, max(0, (seg_end - (row0 + wr * 128) + 15) / 16));
+
     YV_TILE_ISSUE(0, 0);
     if (C::NST == 3 && nks > 1) YV_TILE_ISSUE(1, 1);
     int st = 0;
@@ -872,38 +878,45 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
         }
         const unsigned char* As = lds_a[st];
         const unsigned char* Bs = lds_b[st];
-        bf16x8 bq[2][2];
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-            if constexpr (C::I4) {
-                const u32x2 raw = *(const u32x2*)(Bs + b_rd0[nb]);
-                const float s = bf16_to_f32(lds_s4[brow[nb] * (p.K / 128) + (c * TBK) / 128]);
-                Frag16 f;
-                BLoad<WF>::cvt(make_uint2(raw.x, raw.y), s, f);
-                bq[nb][0] = f.v[0];
-                bq[nb][1] = f.v[1];
-            } else if constexpr (C::EB == 1) {
-                const u32x4 raw = *(const u32x4*)(Bs + b_rd0[nb]);
-                const float s = GROUPED ? lds_s[sblk[nb]][(c * TBK) / 128] : cs[nb];
-                Frag16 f;
-                BLoad<WF>::cvt(make_uint4(raw.x, raw.y, raw.z, raw.w), s, f);
-                bq[nb][0] = f.v[0];
-                bq[nb][1] = f.v[1];
-            } else {
-                bq[nb][0] = *(const bf16x8*)(Bs + b_rd0[nb]);
-                bq[nb][1] = *(const bf16x8*)(Bs + b_rd1[nb]);
-            }
-        }
-#pragma unroll
-        for (int mb = 0; mb < 8; ++mb) {
-            const bf16x8 a0 = *(const bf16x8*)(As + a_rd0 + mb * 16 * 128);
-            const bf16x8 a1 = *(const bf16x8*)(As + a_rd1 + mb * 16 * 128);
+        // one chunk of MFMAs; PART: only the row blocks below seg_end (an expert's last tile)
+        auto compute = [&](auto part) {
+            constexpr bool PART = decltype(part)::value;
+            bf16x8 bq[2][2];
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
-                acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bq[nb][0], acc[mb][nb], 0, 0, 0);
-                acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bq[nb][1], acc[mb][nb], 0, 0, 0);
+                if constexpr (C::I4) {
+                    const u32x2 raw = *(const u32x2*)(Bs + b_rd0[nb]);
+                    const float s = bf16_to_f32(lds_s4[brow[nb] * (p.K / 128) + (c * TBK) / 128]);
+                    Frag16 f;
+                    BLoad<WF>::cvt(make_uint2(raw.x, raw.y), s, f);
+                    bq[nb][0] = f.v[0];
+                    bq[nb][1] = f.v[1];
+                } else if constexpr (C::EB == 1) {
+                    const u32x4 raw = *(const u32x4*)(Bs + b_rd0[nb]);
+                    const float s = GROUPED ? lds_s[sblk[nb]][(c * TBK) / 128] : cs[nb];
+                    Frag16 f;
+                    BLoad<WF>::cvt(make_uint4(raw.x, raw.y, raw.z, raw.w), s, f);
+                    bq[nb][0] = f.v[0];
+                    bq[nb][1] = f.v[1];
+                } else {
+                    bq[nb][0] = *(const bf16x8*)(Bs + b_rd0[nb]);
+                    bq[nb][1] = *(const bf16x8*)(Bs + b_rd1[nb]);
+                }
             }
-        }
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb) {
+                if (PART && mb >= live_mb) continue;
+                const bf16x8 a0 = *(const bf16x8*)(As + a_rd0 + mb * 16 * 128);
+                const bf16x8 a1 = *(const bf16x8*)(As + a_rd1 + mb * 16 * 128);
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bq[nb][0], acc[mb][nb], 0, 0, 0);
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bq[nb][1], acc[mb][nb], 0, 0, 0);
+                }
+            }
+        };
+        if (live_mb == 8) compute(std::false_type{});
+        else if (live_mb > 0) compute(std::true_type{});
         if (++st == C::NST) st = 0;
     }
 #undef YV_TILE_ISSUE
