@@ -28,6 +28,9 @@ profiles/expert_ffn_cfg2_decode_traffic.json and reported when present.
 "rmsnorm": the MoE input norms of the hybrid block (two RMSNorms in one pass) at the decode
 and prefill token counts, HBM roofline of the kernel.
 
+"other_configs": configs[0], [3], [4] (cfg1 fp32, cfg4 W4A16 mixed batch, cfg5 fp8 with skewed
+routing): layer step and grouped FFN, the FFN against both rooflines.
+
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
        python bench.py --pmc-probe {cfg2,cfg3}   (launches only, for counter runs)
 """
@@ -45,6 +48,7 @@ METRIC = "MoE layer tokens/s at 1 GPU; HBM GB/s (decode) & MFMA util % (prefill)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "expert_ffn_cfg2_decode_traffic.json")
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+F32_PEAK_TFLOPS = 157.3
 
 
 def parse():
@@ -58,6 +62,8 @@ def parse():
     ap.add_argument("--no-moegate", action="store_true",
                     help="skip the YvMoEGate router and the layer built with it")
     ap.add_argument("--no-norm", action="store_true", help="skip the MoE input RMSNorm timing")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip cfg1 / cfg4 / cfg5 (layer step and FFN against both rooflines)")
     ap.add_argument("--pmc-probe", choices=["cfg2", "cfg3"], default=None,
                     help="run the calibration copy and 5 expert-FFN launches, nothing timed")
     return ap.parse_args()
@@ -246,6 +252,39 @@ def norm_bench(w, steps, lengths):
     return res
 
 
+def other_configs(names, steps):
+    """The BASELINE configs that are not bench lines (cfg1 fp32 parity layer, cfg4 W4A16 mixed
+    batch, cfg5 fp8 skewed routing): the layer step and the grouped FFN, each FFN priced against
+    both rooflines (algorithmic bytes over 8 TB/s, algorithmic FLOPs over the MFMA peak of the
+    compute dtype: fp32 157.3 TFLOP/s for cfg1, bf16 2.5 PFLOP/s otherwise)."""
+    import torch
+    from pisceslx_amd import functional as yvf
+    from pisceslx_amd.quant import FORMAT_NAMES
+    from pisceslx_amd.workloads import make_workload, mix_weights, router_state
+    res = {}
+    for name in names:
+        w = make_workload(name, device="cuda")
+        spec = w.spec
+        st, mix = router_state(w), mix_weights(w)
+        act = yvf._act(spec.act_dtype)
+        ws = torch.empty(yvf.workspace_bytes(w.n_tokens, act, st, w.experts), dtype=torch.uint8,
+                         device=w.x.device)
+        t = time_layer(yvf, w.x, st, w.experts, mix, None, ws, steps, 3)
+        tf, rt = time_ffn(yvf, w.x, st, w.experts, mix, None, ws, spec.top_k, steps)
+        wk = ffn_work(spec, w.n_tokens, rt)
+        peak = F32_PEAK_TFLOPS if spec.act_dtype == torch.float32 else BF16_PEAK_TFLOPS
+        res[name] = {"tokens": w.n_tokens, "ms_per_step": round(t * 1e3, 4),
+                     "tokens_per_s": round(w.n_tokens / t, 1), "ffn_ms_per_launch": round(tf * 1e3, 4),
+                     "ffn_tflops": round(wk["flops"] / tf / 1e12, 1),
+                     "ffn_mfma_frac": round(wk["flops"] / tf / 1e12 / peak, 4),
+                     "ffn_gbs": round(wk["bytes"] / tf / 1e9, 1),
+                     "ffn_hbm_frac": round(wk["bytes"] / tf / 1e9 / HBM_PEAK_GBS, 4),
+                     "active_experts": wk["active_experts"], "weights": FORMAT_NAMES[spec.fmt]}
+        del w, ws
+        torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(w, budget_s=30.0):
     """The CPU oracle (reference algorithm restated with torch on the host), bounded."""
     import torch
@@ -351,6 +390,8 @@ def main():
         result["moegate"] = moegate_bench(w, mix, args.steps, args.prefill_steps, seq_lengths("cfg3", 0))
     if not args.no_norm:
         result["rmsnorm"] = norm_bench(w, args.steps, seq_lengths("cfg3", 0))
+    if not args.no_other_configs:
+        result["other_configs"] = other_configs(("cfg1", "cfg4", "cfg5"), max(5, args.prefill_steps // 2))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)
