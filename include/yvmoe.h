@@ -5,7 +5,9 @@
  * memory, launches only on the stream it is given (a hipStream_t passed as void*), and
  * returns a yvmoe_status. yvmoe_last_error() returns a thread-local message for the last
  * failure on the calling thread. Scratch memory comes from the caller as a workspace whose
- * size yvmoe_workspace_bytes() reports.
+ * size yvmoe_workspace_bytes() reports. Activations, outputs and workspaces are read and
+ * written in 16-byte vectors: yvmoe_expert_ffn, yvmoe_forward and yvmoe_forward_moegate
+ * reject an x, y / out or workspace pointer that is not 16-byte aligned (YVMOE_ERR_ARG).
  *
  * Reference interfaces replaced (Dunimd-Experimental/PiscesLx):
  *   yvmoe_router_logits  -> YvStableMoEGate.gate(x_flat) and complexity_predictor(x)

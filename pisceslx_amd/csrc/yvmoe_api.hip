@@ -165,6 +165,8 @@ int32_t yvmoe_expert_ffn(const void* x, int32_t act_dtype, int32_t n_tokens, int
                YVMOE_ERR_SHAPE, "top_k=%d invalid", top_k);
     if (n_tokens == 0) return YVMOE_OK;
     YV_REQUIRE(x && y, YVMOE_ERR_ARG, "NULL pointer");
+    YV_REQUIRE(((uintptr_t)x | (uintptr_t)y | (uintptr_t)workspace) % 16 == 0, YVMOE_ERR_ARG,
+               "x, y and workspace must be 16-byte aligned");
     const long long rows = (long long)n_tokens * (top_k + experts->num_shared);
     YV_REQUIRE(rows * experts->hidden < (1ll << 40), YVMOE_ERR_SHAPE, "problem too large");
     const size_t need = route_ws(n_tokens, experts->num_routed, top_k).bytes +
@@ -217,6 +219,8 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
     YV_REQUIRE(workspace != nullptr && workspace_bytes >= need, YVMOE_ERR_WORKSPACE,
                "workspace %zu bytes, need %zu", workspace_bytes, need);
     YV_REQUIRE(n_tokens == 0 || (x && out), YVMOE_ERR_ARG, "NULL pointer");
+    YV_REQUIRE(((uintptr_t)x | (uintptr_t)out | (uintptr_t)workspace) % 16 == 0, YVMOE_ERR_ARG,
+               "x, out and workspace must be 16-byte aligned");
     YV_REQUIRE(experts->num_shared == 0 || mix != nullptr, YVMOE_ERR_ARG,
                "shared experts need mix weights");
     hipStream_t st = (hipStream_t)stream;
@@ -387,6 +391,8 @@ int32_t yvmoe_forward_moegate(const void* x, int32_t act_dtype, int32_t n_tokens
     YV_REQUIRE(n_tokens >= 0, YVMOE_ERR_ARG, "n_tokens=%d < 0", n_tokens);
     YV_REQUIRE(loss != nullptr, YVMOE_ERR_ARG, "loss is NULL");
     YV_REQUIRE(n_tokens == 0 || (x && out && logits), YVMOE_ERR_ARG, "NULL pointer");
+    YV_REQUIRE(((uintptr_t)x | (uintptr_t)out | (uintptr_t)workspace) % 16 == 0, YVMOE_ERR_ARG,
+               "x, out and workspace must be 16-byte aligned");
     YV_REQUIRE(S == 0 || mix != nullptr, YVMOE_ERR_ARG, "shared experts need mix weights");
     YV_REQUIRE(modal_id == nullptr || (gate->modal_affinity && gate->n_modalities > 0),
                YVMOE_ERR_ARG, "modal_id needs modal_affinity");

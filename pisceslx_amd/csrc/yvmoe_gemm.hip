@@ -789,11 +789,21 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
         b_dst[j] = C::I4 ? rb * 512 + half * 256 : blk * 1024;
     }
 
-    // this lane's weight rows in the tile (fragment column l % 16 of each 16-row block)
+    // The weights are the MFMA's first operand: lane l supplies weight row brow[nb] as operand
+    // row i = l % 16 of fragment nb, and its accumulator ends with output row c = l % 16 of
+    // the row block and the columns of operand rows 4 (l / 16) .. + 3. Gate/up: fragment nb
+    // is rows wc 16 + i of the gate (0) or up (1) half, so a lane holds gate and up of the same
+    // 4 columns. Down / fp32 output: the wavefront's 32 rows are dealt out in groups of four,
+    // group q = i / 4 of fragment nb taking rows 8 q + 4 ((q / 2) ^ nb) + i % 4, so that lane l
+    // holds the 8 consecutive columns 8 (l / 16) .. + 7 (fragment 0 first for l < 32) and the
+    // epilogue writes 16 bytes per lane; the LDS reads of a fragment still cover 16 distinct
+    // 16-byte bank groups per 16 lanes.
     int brow[2];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-        brow[nb] = SWIGLU ? nb * (TBN / 2) + wc * 16 + (lane & 15) : wc * 32 + nb * 16 + (lane & 15);
+    for (int nb = 0; nb < 2; ++nb) {
+        const int i = lane & 15, q = i >> 2;
+        brow[nb] = SWIGLU ? nb * (TBN / 2) + wc * 16 + i : wc * 32 + q * 8 + 4 * ((q >> 1) ^ nb) + (i & 3);
+    }
     float cs[2] = {1.0f, 1.0f};  // int8: per-column scales
     int sblk[2] = {0, 0};        // fp8: which of the tile's two scale blocks
     if constexpr (WF == YVMOE_W_INT8) {
@@ -837,8 +847,8 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     const int a_rd0 = swz_a(wr * 128 + (lane & 15), 2 * g), a_rd1 = swz_a(wr * 128 + (lane & 15), 2 * g + 1);
     int b_rd0[2], b_rd1[2];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {  // piece (g, r) of the row's block: lane * 16 (+ 1 KB)
-        b_rd0[nb] = (brow[nb] >> 4) * C::B_BLK + lane * (C::I4 ? 8 : 16);
+    for (int nb = 0; nb < 2; ++nb) {  // piece (g, row % 16) of the row's block (+ 1 KB)
+        b_rd0[nb] = (brow[nb] >> 4) * C::B_BLK + (16 * g + (brow[nb] & 15)) * (C::I4 ? 8 : 16);
         b_rd1[nb] = b_rd0[nb] + 1024;
     }
 
@@ -910,8 +920,8 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
                 const bf16x8 a1 = *(const bf16x8*)(As + a_rd1 + mb * 16 * 128);
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) {
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bq[nb][0], acc[mb][nb], 0, 0, 0);
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bq[nb][1], acc[mb][nb], 0, 0, 0);
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][0], a0, acc[mb][nb], 0, 0, 0);
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][1], a1, acc[mb][nb], 0, 0, 0);
                 }
             }
         };
@@ -921,31 +931,38 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     }
 #undef YV_TILE_ISSUE
 
-    // epilogue: lane holds rows 4*(l/16)+i of each 16-row block, column l%16 of each block
+    // epilogue: row l % 16 of each 16-row block; gate/up 4 consecutive columns (8-byte
+    // stores), down 8 (16-byte stores)
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
+        const int r = row0 + wr * 128 + mb * 16 + (lane & 15);
+        if (r >= seg_end) continue;
+        if constexpr (SWIGLU) {
+            const int n = n0 + wc * 16 + 4 * g;
+            float hv[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = row0 + wr * 128 + mb * 16 + (lane >> 4) * 4 + i;
-            if (r >= seg_end) continue;
-            if constexpr (SWIGLU) {
-                const int n = n0 + wc * 16 + (lane & 15);
+            for (int i = 0; i < 4; ++i) {
                 const float gt = round_bf16(acc[mb][0][i]);
                 const float up = round_bf16(acc[mb][1][i]);
-                const float sgl = round_bf16(silu(gt));
-                ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(sgl * up);
-            } else if constexpr (EPI == EPI_F32) {
+                hv[i] = round_bf16(silu(gt)) * up;
+            }
+            *(uint2*)((unsigned short*)p.out + (long long)r * p.ldo + n) =
+                make_uint2(pack_bf16(hv[0], hv[1]), pack_bf16(hv[2], hv[3]));
+        } else {
+            const int n = n0 + wc * 32 + 8 * g;
+            const f32x4 lo = g < 2 ? acc[mb][0] : acc[mb][1];
+            const f32x4 hi = g < 2 ? acc[mb][1] : acc[mb][0];
+            if constexpr (EPI == EPI_F32) {
+                float* o = (float*)p.out + (long long)r * p.ldo + n;
 #pragma unroll
-                for (int nb = 0; nb < 2; ++nb) {
-                    const int n = n0 + wc * 32 + nb * 16 + (lane & 15);
-                    ((float*)p.out)[(long long)r * p.ldo + n] = f32_out(p, acc[mb][nb][i], n, 0);
+                for (int i = 0; i < 4; ++i) {
+                    o[i] = f32_out(p, lo[i], n + i, 0);
+                    o[4 + i] = f32_out(p, hi[i], n + 4 + i, 0);
                 }
             } else {
-#pragma unroll
-                for (int nb = 0; nb < 2; ++nb) {
-                    const int n = n0 + wc * 32 + nb * 16 + (lane & 15);
-                    ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(acc[mb][nb][i]);
-                }
+                *(uint4*)((unsigned short*)p.out + (long long)r * p.ldo + n) =
+                    make_uint4(pack_bf16(lo[0], lo[1]), pack_bf16(lo[2], lo[3]),
+                               pack_bf16(hi[0], hi[1]), pack_bf16(hi[2], hi[3]));
             }
         }
     }

@@ -157,3 +157,33 @@ def test_forward_is_deterministic(cuda, oracle):
     a = yvf.moe_forward(w.x, st, w.experts, mix, None)[0]
     b = yvf.moe_forward(w.x, st, w.experts, mix, None)[0]
     assert torch.equal(a, b)
+
+
+def test_misaligned_pointers_rejected(cuda):
+    """x, y / out and the workspace are accessed in 16-byte vectors: the FFN entry points
+    reject pointers that are not 16-byte aligned before launching anything."""
+    import ctypes
+
+    from pisceslx_amd import _lib
+    w = make_workload("cfg2", device=cuda, n_tokens=8)
+    st, mix = router_state(w), mix_weights(w)
+    N, H = w.x.shape
+    ws = torch.empty(yvf.workspace_bytes(N, _lib.ACT_BF16, st, w.experts) + 64, dtype=torch.uint8,
+                     device=cuda)
+    out, _, routing = yvf.moe_forward(w.x, st, w.experts, mix, None, workspace=ws)
+    y = torch.empty(N * (w.spec.top_k + w.spec.num_shared) + 1, H, dtype=torch.bfloat16, device=cuda)
+    e, o, r = w.experts.struct(), routing.struct(), st.struct()
+    stream = torch.cuda.current_stream().cuda_stream
+    lib = _lib.lib()
+    for xp, yp, wp in ((w.x.data_ptr() + 2, y.data_ptr(), ws.data_ptr()),
+                       (w.x.data_ptr(), y.data_ptr() + 8, ws.data_ptr()),
+                       (w.x.data_ptr(), y.data_ptr(), ws.data_ptr() + 4)):
+        rc = lib.yvmoe_expert_ffn(xp, _lib.ACT_BF16, N, w.spec.top_k, ctypes.byref(e), ctypes.byref(o),
+                                  yp, wp, ws.numel() - 8, stream)
+        assert rc == _lib.YVMOE_ERR_ARG and b"16-byte" in lib.yvmoe_last_error()
+        rc = lib.yvmoe_forward(xp, _lib.ACT_BF16, N, ctypes.byref(r), ctypes.byref(e), mix.data_ptr(),
+                               None, yp, None, ctypes.byref(o), wp, ws.numel() - 8, stream)
+        assert rc == _lib.YVMOE_ERR_ARG and b"16-byte" in lib.yvmoe_last_error()
+    torch.cuda.synchronize()
+    ref, _, _ = yvf.moe_forward(w.x, st, w.experts, mix, None, workspace=ws)
+    assert torch.equal(ref, out)
