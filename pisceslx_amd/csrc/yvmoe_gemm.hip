@@ -706,28 +706,40 @@ __device__ __forceinline__ int swz_a(int r, int c) {  // bytes, 128-byte rows
 // 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima)
 constexpr int vmcnt_only(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
 
-template <int WF>
+// FOLD: room for the kTileFold rows of a folded remainder. S4K: int4 only, the largest K whose
+// group scales the LDS table holds (8192; with folded rows 5120 beside a 3-stage ring, 8192
+// beside a 2-stage ring).
+template <int WF, int S4K = 8192, bool FOLD = false>
 struct TileCfg {
     static constexpr bool I4 = WF == YVMOE_W_INT4;
     static constexpr int EB = (WF == YVMOE_W_BF16) ? 2 : 1;  // bytes per weight (int4: half)
-    static constexpr int NST = (EB == 2) ? 2 : 3;             // LDS stages (160 KB of LDS)
-    static constexpr int A_BYTES = TBM * TBK * 2;
+    // LDS stages (160 KB of LDS)
+    static constexpr int NST = (EB == 2 || (I4 && FOLD && S4K > 5120)) ? 2 : 3;
+    // activation rows: the 256-row tile (and the rows a folded remainder adds)
+    static constexpr int A_BYTES = (TBM + (FOLD ? kTileFold : 0)) * TBK * 2;
     static constexpr int B_BYTES = I4 ? TBN * TBK / 2 : TBN * TBK * EB;
     static constexpr int B_BLK = I4 ? 512 : 1024 * EB;  // bytes of a 16-row weight block
-    static constexpr int A_DMA = A_BYTES / 1024 / (TTHREADS / 64);  // 1 KB direct loads per wavefront
+    // 1 KB direct loads per wavefront for the 256 rows; the 32 folded rows take one 256-byte
+    // dword load per wavefront, issued only by tiles that hold such rows
+    static constexpr int A_DMA = TBM * TBK * 2 / 1024 / (TTHREADS / 64);
     // weight direct loads per wavefront: 1 KB each (int4: 256 B dword loads, two per block)
     static constexpr int B_DMA = I4 ? 2 : B_BYTES / 1024 / (TTHREADS / 64);
     static constexpr int NPW = A_DMA + B_DMA;
-    static constexpr int S4 = I4 ? TBN * 64 : 1;  // int4: the tile's group scales, K <= 8192
+    static constexpr int S4 = I4 ? TBN * (S4K / 128) : 1;  // int4: the tile's group scales
 };
+static_assert(kTileFold * TBK * 2 == 256 * (TTHREADS / 64), "one dword load per wavefront");
 
 // Work items are (tile, column block) pairs, column block fastest, so the work-groups that
 // run together share activation tiles and (mostly) one expert's weights. Consecutive
 // work-group ids go to different XCDs (round-robin dispatch), so the item space is cut into 8
 // contiguous ranges, one per XCD, to keep each XCD's L2 traffic on its own range.
-template <int WF, int EPI>
+// FOLD: the tile table folds remainders, so an expert's last tile may hold 256 + 1 .. kTileFold
+// rows. Such a launch holds two copies of the tile loop and each work-group runs the one its
+// tile needs: the copy without folded rows keeps the register use and schedule of a plain
+// tile. Launches without folding (FOLD = false) carry only that copy.
+template <int WF, int EPI, int S4K = 8192, bool FOLD = false>
 __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int ncb) {
-    typedef TileCfg<WF> C;
+    typedef TileCfg<WF, S4K, FOLD> C;
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
     constexpr bool GROUPED = WF == YVMOE_W_FP8;
     constexpr long long B_CHUNK = C::B_BLK;  // bytes of a weight block (64-wide K step)
@@ -759,213 +771,260 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     const long long e_off = (long long)e * p.b_stride;
     const long long s_off = (long long)e * p.s_stride;
 
-    // direct-load sources: activation block j of this wavefront holds tile rows 8 (A_DMA w + j)
-    // .. + 7, lane L row + L / 8, logical chunk (L % 8) ^ (L / 8) ^ (block & 1)
-    const char* a_src[C::A_DMA];
-#pragma unroll
-    for (int j = 0; j < C::A_DMA; ++j) {
-        const int blk = wave * C::A_DMA + j;
-        const int r = blk * 8 + lane / 8;
-        const int lc = (lane % 8) ^ (lane / 8) ^ (blk & 1);
-        const int gr = (row0 + r < seg_end) ? row0 + r : row0;
-        a_src[j] = (const char*)p.A + ((long long)map_row(p, gr) * p.lda + lc * 8) * 2;
-    }
-    // weight blocks: 16-row x 64-column blocks (1 KB per 1-byte block, two 1 KB halves per
-    // bf16 block) land in LDS as stored, block after block
-    // (int4: 512-byte blocks, each loaded as two 256-byte halves by one wavefront)
-    const char* b_src[C::B_DMA];
-    int b_dst[C::B_DMA];
-#pragma unroll
-    for (int j = 0; j < C::B_DMA; ++j) {
-        const int blk = wave * C::B_DMA + j;
-        const int rb = C::I4 ? wave : blk / C::EB;           // 16-row block of the tile
-        const int half = C::I4 ? j : blk % C::EB;
-        const int r16 = rb * 16;
-        const void* B = (SWIGLU && r16 >= TBN / 2) ? p.B1 : p.B0;
-        const int nb16 = SWIGLU ? n0 + (r16 & (TBN / 2 - 1)) : n0 + r16;
-        const long long e_bytes = C::I4 ? e_off / 2 : e_off * C::EB;
-        b_src[j] = (const char*)B + e_bytes + (long long)(nb16 >> 4) * (p.K / 64) * B_CHUNK +
-                   (C::I4 ? half * 256 + lane * 4 : half * 1024 + lane * 16);
-        b_dst[j] = C::I4 ? rb * 512 + half * 256 : blk * 1024;
-    }
+    // rows past the 256-row tile: an expert's last tile that holds a folded remainder
+    // (1 .. kTileFold rows; a folding tile table leaves no larger gap to the next tile)
+    const int ext = FOLD && !dense ? seg_end - row0 - TBM : 0;
 
-    // The weights are the MFMA's first operand: lane l supplies weight row brow[nb] as operand
-    // row i = l % 16 of fragment nb, and its accumulator ends with output row c = l % 16 of
-    // the row block and the columns of operand rows 4 (l / 16) .. + 3. Gate/up: fragment nb
-    // is rows wc 16 + i of the gate (0) or up (1) half, so a lane holds gate and up of the same
-    // 4 columns. Down / fp32 output: the wavefront's 32 rows are dealt out in groups of four,
-    // group q = i / 4 of fragment nb taking rows 8 q + 4 ((q / 2) ^ nb) + i % 4, so that lane l
-    // holds the 8 consecutive columns 8 (l / 16) .. + 7 (fragment 0 first for l < 32) and the
-    // epilogue writes 16 bytes per lane; the LDS reads of a fragment still cover 16 distinct
-    // 16-byte bank groups per 16 lanes.
-    int brow[2];
+    auto run_tile = [&](auto fold_tag) {
+        constexpr bool XT = decltype(fold_tag)::value;
+
+        // direct-load sources: activation block j of this wavefront holds tile rows 8 (A_DMA w + j)
+        // .. + 7, lane L row + L / 8, logical chunk (L % 8) ^ (L / 8) ^ (block & 1)
+        const char* a_src[C::A_DMA];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-        const int i = lane & 15, q = i >> 2;
-        brow[nb] = SWIGLU ? nb * (TBN / 2) + wc * 16 + i : wc * 32 + q * 8 + 4 * ((q >> 1) ^ nb) + (i & 3);
-    }
-    float cs[2] = {1.0f, 1.0f};  // int8: per-column scales
-    int sblk[2] = {0, 0};        // fp8: which of the tile's two scale blocks
-    if constexpr (WF == YVMOE_W_INT8) {
+        for (int j = 0; j < C::A_DMA; ++j) {
+            const int blk = wave * C::A_DMA + j;
+            const int r = blk * 8 + lane / 8;
+            const int lc = (lane % 8) ^ (lane / 8) ^ (blk & 1);
+            const int gr = (row0 + r < seg_end) ? row0 + r : row0;
+            a_src[j] = (const char*)p.A + ((long long)map_row(p, gr) * p.lda + lc * 8) * 2;
+        }
+        // folded rows: wavefront w loads rows 256 + 2 w and + 1, lane L dword L % 4 of physical
+        // chunk (L % 32) / 4 of row 256 + 2 w + L / 32 (the same swizzle as the other rows)
+        const char* x_src;
+        {
+            const int r = TBM + 2 * wave + lane / 32;
+            const int lc = ((lane % 32) / 4) ^ (r & 7) ^ ((r >> 3) & 1);
+            const int gr = (row0 + r < seg_end) ? row0 + r : row0;
+            x_src = (const char*)p.A + ((long long)map_row(p, gr) * p.lda + lc * 8) * 2 + (lane % 4) * 4;
+        }
+        // weight blocks: 16-row x 64-column blocks (1 KB per 1-byte block, two 1 KB halves per
+        // bf16 block) land in LDS as stored, block after block
+        // (int4: 512-byte blocks, each loaded as two 256-byte halves by one wavefront)
+        const char* b_src[C::B_DMA];
+        int b_dst[C::B_DMA];
+#pragma unroll
+        for (int j = 0; j < C::B_DMA; ++j) {
+            const int blk = wave * C::B_DMA + j;
+            const int rb = C::I4 ? wave : blk / C::EB;           // 16-row block of the tile
+            const int half = C::I4 ? j : blk % C::EB;
+            const int r16 = rb * 16;
+            const void* B = (SWIGLU && r16 >= TBN / 2) ? p.B1 : p.B0;
+            const int nb16 = SWIGLU ? n0 + (r16 & (TBN / 2 - 1)) : n0 + r16;
+            const long long e_bytes = C::I4 ? e_off / 2 : e_off * C::EB;
+            b_src[j] = (const char*)B + e_bytes + (long long)(nb16 >> 4) * (p.K / 64) * B_CHUNK +
+                       (C::I4 ? half * 256 + lane * 4 : half * 1024 + lane * 16);
+            b_dst[j] = C::I4 ? rb * 512 + half * 256 : blk * 1024;
+        }
+
+        // The weights are the MFMA's first operand: lane l supplies weight row brow[nb] as operand
+        // row i = l % 16 of fragment nb, and its accumulator ends with output row c = l % 16 of
+        // the row block and the columns of operand rows 4 (l / 16) .. + 3. Gate/up: fragment nb
+        // is rows wc 16 + i of the gate (0) or up (1) half, so a lane holds gate and up of the same
+        // 4 columns. Down / fp32 output: the wavefront's 32 rows are dealt out in groups of four,
+        // group q = i / 4 of fragment nb taking rows 8 q + 4 ((q / 2) ^ nb) + i % 4, so that lane l
+        // holds the 8 consecutive columns 8 (l / 16) .. + 7 (fragment 0 first for l < 32) and the
+        // epilogue writes 16 bytes per lane; the LDS reads of a fragment still cover 16 distinct
+        // 16-byte bank groups per 16 lanes.
+        int brow[2];
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-            const int r = brow[nb];
-            const void* S = (SWIGLU && r >= TBN / 2) ? p.S1 : p.S0;
-            cs[nb] = b_scale<WF>(S, s_off, SWIGLU ? n0 + (r & (TBN / 2 - 1)) : n0 + r, p.K, 0);
+            const int i = lane & 15, q = i >> 2;
+            brow[nb] = SWIGLU ? nb * (TBN / 2) + wc * 16 + i : wc * 32 + q * 8 + 4 * ((q >> 1) ^ nb) + (i & 3);
         }
-    }
-    if constexpr (C::I4) {
-        // the tile's group scales into LDS before any direct load is in flight
-        const int kg = p.K / 128;
-        for (int i = t; i < TBN * kg; i += TTHREADS) {
-            const int r = i / kg, q = i % kg;
-            const void* S = (SWIGLU && r >= TBN / 2) ? p.S1 : p.S0;
-            const int n = SWIGLU ? n0 + (r & (TBN / 2 - 1)) : n0 + r;
-            lds_s4[i] = ((const unsigned short*)S)[s_off + (long long)n * kg + q];
-        }
-        __syncthreads();
-    }
-    if constexpr (GROUPED) {
-        const int kb = p.K / 128;
-        if (t < 2 * kb) {
-            const int b = t / kb, q = t % kb;
-            const void* S = (SWIGLU && b == 1) ? p.S1 : p.S0;
-            const int n = SWIGLU ? n0 : n0 + b * 128;
-            lds_s[b][q] = b_scale<WF>(S, s_off, n, p.K, q * 128);
-        }
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) sblk[nb] = brow[nb] / 128;
-        __syncthreads();
-    }
-
-    f32x4 acc[8][2];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    // LDS byte offsets of this lane's fragment reads (k group g = lane / 16)
-    const int g = lane >> 4;
-    const int a_rd0 = swz_a(wr * 128 + (lane & 15), 2 * g), a_rd1 = swz_a(wr * 128 + (lane & 15), 2 * g + 1);
-    int b_rd0[2], b_rd1[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {  // piece (g, row % 16) of the row's block (+ 1 KB)
-        b_rd0[nb] = (brow[nb] >> 4) * C::B_BLK + (16 * g + (brow[nb] & 15)) * (C::I4 ? 8 : 16);
-        b_rd1[nb] = b_rd0[nb] + 1024;
-    }
-
-    // The direct loads are issued from inline assembly: the compiler's own form of them makes
-    // it wait for every outstanding direct load before each LDS read, which would serialize
-    // the prefetch. Completion is tracked here instead, with explicit vmcnt waits.
-#define YV_TILE_ISSUE(CHUNK, ST)                                                                       \
-    do {                                                                                               \
-        _Pragma("unroll") for (int j = 0; j < C::A_DMA; ++j)                                           \
-            dma16(a_src[j] + (size_t)(CHUNK) * TBK * 2, &lds_a[ST][(wave * C::A_DMA + j) * 1024]);     \
-        _Pragma("unroll") for (int j = 0; j < C::B_DMA; ++j) {                                         \
-            if constexpr (C::I4) dma4(b_src[j] + (size_t)(CHUNK) * B_CHUNK, &lds_b[ST][b_dst[j]]);     \
-            else dma16(b_src[j] + (size_t)(CHUNK) * B_CHUNK, &lds_b[ST][b_dst[j]]);                    \
-        }                                                                                              \
-    } while (0)
-
-    // 16-row blocks of this wavefront's 128 rows that hold rows of the segment: an expert's
-    // last tile skips the MFMAs of the blocks past its end (loads and barriers stay uniform)
-    const int live_mb = min(8, max(0, (seg_end - (row0 + wr * 128) + 15) / 16));
-
-    YV_TILE_ISSUE(0, 0);
-    if (C::NST == 3 && nks > 1) YV_TILE_ISSUE(1, 1);
-    int st = 0;
-    for (int c = 0; c < nks; ++c) {
-        // this wavefront's loads of chunk c have landed (the next chunk's may be in flight) ...
-        if (C::NST == 3 && c + 1 < nks) __builtin_amdgcn_s_waitcnt(vmcnt_only(C::NPW));
-        else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-        // ... and after the barrier every wavefront's have, and all reads of chunk c - 1 are
-        // done, so its stage can take chunk c + NST - 1
-        asm volatile("" ::: "memory");
-        __builtin_amdgcn_s_barrier();
-        asm volatile("" ::: "memory");
-        if (c + C::NST - 1 < nks) {
-            int sn = st + C::NST - 1;
-            if (sn >= C::NST) sn -= C::NST;
-            YV_TILE_ISSUE(c + C::NST - 1, sn);
-        }
-        const unsigned char* As = lds_a[st];
-        const unsigned char* Bs = lds_b[st];
-        // one chunk of MFMAs; PART: only the row blocks below seg_end (an expert's last tile)
-        auto compute = [&](auto part) {
-            constexpr bool PART = decltype(part)::value;
-            bf16x8 bq[2][2];
+        float cs[2] = {1.0f, 1.0f};  // int8: per-column scales
+        int sblk[2] = {0, 0};        // fp8: which of the tile's two scale blocks
+        if constexpr (WF == YVMOE_W_INT8) {
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
-                if constexpr (C::I4) {
-                    const u32x2 raw = *(const u32x2*)(Bs + b_rd0[nb]);
-                    const float s = bf16_to_f32(lds_s4[brow[nb] * (p.K / 128) + (c * TBK) / 128]);
-                    Frag16 f;
-                    BLoad<WF>::cvt(make_uint2(raw.x, raw.y), s, f);
-                    bq[nb][0] = f.v[0];
-                    bq[nb][1] = f.v[1];
-                } else if constexpr (C::EB == 1) {
-                    const u32x4 raw = *(const u32x4*)(Bs + b_rd0[nb]);
-                    const float s = GROUPED ? lds_s[sblk[nb]][(c * TBK) / 128] : cs[nb];
-                    Frag16 f;
-                    BLoad<WF>::cvt(make_uint4(raw.x, raw.y, raw.z, raw.w), s, f);
-                    bq[nb][0] = f.v[0];
-                    bq[nb][1] = f.v[1];
-                } else {
-                    bq[nb][0] = *(const bf16x8*)(Bs + b_rd0[nb]);
-                    bq[nb][1] = *(const bf16x8*)(Bs + b_rd1[nb]);
-                }
+                const int r = brow[nb];
+                const void* S = (SWIGLU && r >= TBN / 2) ? p.S1 : p.S0;
+                cs[nb] = b_scale<WF>(S, s_off, SWIGLU ? n0 + (r & (TBN / 2 - 1)) : n0 + r, p.K, 0);
+            }
+        }
+        if constexpr (C::I4) {
+            // the tile's group scales into LDS before any direct load is in flight
+            const int kg = p.K / 128;
+            for (int i = t; i < TBN * kg; i += TTHREADS) {
+                const int r = i / kg, q = i % kg;
+                const void* S = (SWIGLU && r >= TBN / 2) ? p.S1 : p.S0;
+                const int n = SWIGLU ? n0 + (r & (TBN / 2 - 1)) : n0 + r;
+                lds_s4[i] = ((const unsigned short*)S)[s_off + (long long)n * kg + q];
+            }
+            __syncthreads();
+        }
+        if constexpr (GROUPED) {
+            const int kb = p.K / 128;
+            if (t < 2 * kb) {
+                const int b = t / kb, q = t % kb;
+                const void* S = (SWIGLU && b == 1) ? p.S1 : p.S0;
+                const int n = SWIGLU ? n0 : n0 + b * 128;
+                lds_s[b][q] = b_scale<WF>(S, s_off, n, p.K, q * 128);
             }
 #pragma unroll
-            for (int mb = 0; mb < 8; ++mb) {
-                if (PART && mb >= live_mb) continue;
-                const bf16x8 a0 = *(const bf16x8*)(As + a_rd0 + mb * 16 * 128);
-                const bf16x8 a1 = *(const bf16x8*)(As + a_rd1 + mb * 16 * 128);
+            for (int nb = 0; nb < 2; ++nb) sblk[nb] = brow[nb] / 128;
+            __syncthreads();
+        }
+
+        f32x4 acc[8][2];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        // LDS byte offsets of this lane's fragment reads (k group g = lane / 16)
+        const int g = lane >> 4;
+        const int a_rd0 = swz_a(wr * 128 + (lane & 15), 2 * g), a_rd1 = swz_a(wr * 128 + (lane & 15), 2 * g + 1);
+        int b_rd0[2], b_rd1[2];
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {  // piece (g, row % 16) of the row's block (+ 1 KB)
+            b_rd0[nb] = (brow[nb] >> 4) * C::B_BLK + (16 * g + (brow[nb] & 15)) * (C::I4 ? 8 : 16);
+            b_rd1[nb] = b_rd0[nb] + 1024;
+        }
+
+        // The direct loads are issued from inline assembly: the compiler's own form of them makes
+        // it wait for every outstanding direct load before each LDS read, which would serialize
+        // the prefetch. Completion is tracked here instead, with explicit vmcnt waits.
+#define YV_TILE_ISSUE(CHUNK, ST)                                                                       \
+        do {                                                                                               \
+            _Pragma("unroll") for (int j = 0; j < C::A_DMA; ++j)                                           \
+                dma16(a_src[j] + (size_t)(CHUNK) * TBK * 2, &lds_a[ST][(wave * C::A_DMA + j) * 1024]);     \
+            if (XT) dma4(x_src + (size_t)(CHUNK) * TBK * 2, &lds_a[ST][TBM * TBK * 2 + wave * 256]);      \
+            _Pragma("unroll") for (int j = 0; j < C::B_DMA; ++j) {                                         \
+                if constexpr (C::I4) dma4(b_src[j] + (size_t)(CHUNK) * B_CHUNK, &lds_b[ST][b_dst[j]]);     \
+                else dma16(b_src[j] + (size_t)(CHUNK) * B_CHUNK, &lds_b[ST][b_dst[j]]);                    \
+            }                                                                                              \
+        } while (0)
+
+        // 16-row blocks of this wavefront's 128 rows that hold rows of the segment: an expert's
+        // last tile skips the MFMAs of the blocks past its end (loads and barriers stay uniform)
+        const int live_mb = min(8, max(0, (seg_end - (row0 + wr * 128) + 15) / 16));
+        // folded rows: wavefront row wr computes row block 256 + 16 wr .. + 15 when it holds rows
+        const bool xlive = XT && ext > 16 * wr;
+        f32x4 accx[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+        const int xa_rd0 = swz_a(TBM + wr * 16 + (lane & 15), 2 * g);
+        const int xa_rd1 = swz_a(TBM + wr * 16 + (lane & 15), 2 * g + 1);
+
+        YV_TILE_ISSUE(0, 0);
+        if (C::NST == 3 && nks > 1) YV_TILE_ISSUE(1, 1);
+        int st = 0;
+        for (int c = 0; c < nks; ++c) {
+            // this wavefront's loads of chunk c have landed (the next chunk's may be in flight) ...
+            if (C::NST == 3 && c + 1 < nks) {
+                if (XT) __builtin_amdgcn_s_waitcnt(vmcnt_only(C::NPW + 1));
+                else __builtin_amdgcn_s_waitcnt(vmcnt_only(C::NPW));
+            } else {
+                __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+            }
+            // ... and after the barrier every wavefront's have, and all reads of chunk c - 1 are
+            // done, so its stage can take chunk c + NST - 1
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            if (c + C::NST - 1 < nks) {
+                int sn = st + C::NST - 1;
+                if (sn >= C::NST) sn -= C::NST;
+                YV_TILE_ISSUE(c + C::NST - 1, sn);
+            }
+            const unsigned char* As = lds_a[st];
+            const unsigned char* Bs = lds_b[st];
+            // one chunk of MFMAs; PART: only the row blocks below seg_end (an expert's last tile);
+            // EXT: plus the folded row block
+            auto compute = [&](auto part, auto extra) {
+                constexpr bool PART = decltype(part)::value;
+                constexpr bool EXT = decltype(extra)::value;
+                bf16x8 bq[2][2];
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) {
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][0], a0, acc[mb][nb], 0, 0, 0);
-                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][1], a1, acc[mb][nb], 0, 0, 0);
+                    if constexpr (C::I4) {
+                        const u32x2 raw = *(const u32x2*)(Bs + b_rd0[nb]);
+                        const float s = bf16_to_f32(lds_s4[brow[nb] * (p.K / 128) + (c * TBK) / 128]);
+                        Frag16 f;
+                        BLoad<WF>::cvt(make_uint2(raw.x, raw.y), s, f);
+                        bq[nb][0] = f.v[0];
+                        bq[nb][1] = f.v[1];
+                    } else if constexpr (C::EB == 1) {
+                        const u32x4 raw = *(const u32x4*)(Bs + b_rd0[nb]);
+                        const float s = GROUPED ? lds_s[sblk[nb]][(c * TBK) / 128] : cs[nb];
+                        Frag16 f;
+                        BLoad<WF>::cvt(make_uint4(raw.x, raw.y, raw.z, raw.w), s, f);
+                        bq[nb][0] = f.v[0];
+                        bq[nb][1] = f.v[1];
+                    } else {
+                        bq[nb][0] = *(const bf16x8*)(Bs + b_rd0[nb]);
+                        bq[nb][1] = *(const bf16x8*)(Bs + b_rd1[nb]);
+                    }
+                }
+#pragma unroll
+                for (int mb = 0; mb < 8; ++mb) {
+                    if (PART && mb >= live_mb) continue;
+                    const bf16x8 a0 = *(const bf16x8*)(As + a_rd0 + mb * 16 * 128);
+                    const bf16x8 a1 = *(const bf16x8*)(As + a_rd1 + mb * 16 * 128);
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb) {
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][0], a0, acc[mb][nb], 0, 0, 0);
+                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][1], a1, acc[mb][nb], 0, 0, 0);
+                    }
+                }
+                if constexpr (EXT) {
+                    const bf16x8 a0 = *(const bf16x8*)(As + xa_rd0);
+                    const bf16x8 a1 = *(const bf16x8*)(As + xa_rd1);
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb) {
+                        accx[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][0], a0, accx[nb], 0, 0, 0);
+                        accx[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][1], a1, accx[nb], 0, 0, 0);
+                    }
+                }
+            };
+            if (xlive) compute(std::false_type{}, std::true_type{});
+            else if (live_mb == 8) compute(std::false_type{}, std::false_type{});
+            else if (live_mb > 0) compute(std::true_type{}, std::false_type{});
+            if (++st == C::NST) st = 0;
+        }
+#undef YV_TILE_ISSUE
+
+        // epilogue: row l % 16 of each 16-row block; gate/up 4 consecutive columns (8-byte
+        // stores), down 8 (16-byte stores)
+        auto store = [&](int r, f32x4 c0, f32x4 c1) {
+            if constexpr (SWIGLU) {
+                const int n = n0 + wc * 16 + 4 * g;
+                float hv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float gt = round_bf16(c0[i]);
+                    const float up = round_bf16(c1[i]);
+                    hv[i] = round_bf16(silu(gt)) * up;
+                }
+                *(uint2*)((unsigned short*)p.out + (long long)r * p.ldo + n) =
+                    make_uint2(pack_bf16(hv[0], hv[1]), pack_bf16(hv[2], hv[3]));
+            } else {
+                const int n = n0 + wc * 32 + 8 * g;
+                const f32x4 lo = g < 2 ? c0 : c1;
+                const f32x4 hi = g < 2 ? c1 : c0;
+                if constexpr (EPI == EPI_F32) {
+                    float* o = (float*)p.out + (long long)r * p.ldo + n;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        o[i] = f32_out(p, lo[i], n + i, 0);
+                        o[4 + i] = f32_out(p, hi[i], n + 4 + i, 0);
+                    }
+                } else {
+                    *(uint4*)((unsigned short*)p.out + (long long)r * p.ldo + n) =
+                        make_uint4(pack_bf16(lo[0], lo[1]), pack_bf16(lo[2], lo[3]),
+                                   pack_bf16(hi[0], hi[1]), pack_bf16(hi[2], hi[3]));
                 }
             }
         };
-        if (live_mb == 8) compute(std::false_type{});
-        else if (live_mb > 0) compute(std::true_type{});
-        if (++st == C::NST) st = 0;
-    }
-#undef YV_TILE_ISSUE
-
-    // epilogue: row l % 16 of each 16-row block; gate/up 4 consecutive columns (8-byte
-    // stores), down 8 (16-byte stores)
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) {
-        const int r = row0 + wr * 128 + mb * 16 + (lane & 15);
-        if (r >= seg_end) continue;
-        if constexpr (SWIGLU) {
-            const int n = n0 + wc * 16 + 4 * g;
-            float hv[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const float gt = round_bf16(acc[mb][0][i]);
-                const float up = round_bf16(acc[mb][1][i]);
-                hv[i] = round_bf16(silu(gt)) * up;
-            }
-            *(uint2*)((unsigned short*)p.out + (long long)r * p.ldo + n) =
-                make_uint2(pack_bf16(hv[0], hv[1]), pack_bf16(hv[2], hv[3]));
-        } else {
-            const int n = n0 + wc * 32 + 8 * g;
-            const f32x4 lo = g < 2 ? acc[mb][0] : acc[mb][1];
-            const f32x4 hi = g < 2 ? acc[mb][1] : acc[mb][0];
-            if constexpr (EPI == EPI_F32) {
-                float* o = (float*)p.out + (long long)r * p.ldo + n;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    o[i] = f32_out(p, lo[i], n + i, 0);
-                    o[4 + i] = f32_out(p, hi[i], n + 4 + i, 0);
-                }
-            } else {
-                *(uint4*)((unsigned short*)p.out + (long long)r * p.ldo + n) =
-                    make_uint4(pack_bf16(lo[0], lo[1]), pack_bf16(lo[2], lo[3]),
-                               pack_bf16(hi[0], hi[1]), pack_bf16(hi[2], hi[3]));
-            }
+        for (int mb = 0; mb < 8; ++mb) {
+            const int r = row0 + wr * 128 + mb * 16 + (lane & 15);
+            if (r < seg_end) store(r, acc[mb][0], acc[mb][1]);
         }
-    }
+        if (xlive) {
+            const int r = row0 + TBM + wr * 16 + (lane & 15);
+            if (r < seg_end) store(r, accx[0], accx[1]);
+        }
+    };
+    if (FOLD && ext > 0 && ext <= kTileFold) run_tile(std::integral_constant<bool, FOLD>{});
+    else run_tile(std::false_type{});
 }
 
 // ------------------------------------------------------------------ fp32 activations
@@ -1067,7 +1126,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
 // rows each after the N*k routed rows. Every segment is cut into 64-row tiles.
 __global__ __launch_bounds__(512) void build_tiles_kernel(const int* __restrict__ offsets, int E,
                                                           int S, int N, int k, int tile_rows,
-                                                          int* __restrict__ seg,
+                                                          int fold, int* __restrict__ seg,
                                                           int* __restrict__ tile_seg,
                                                           int* __restrict__ tile_row0,
                                                           int* __restrict__ ntiles) {
@@ -1085,7 +1144,7 @@ __global__ __launch_bounds__(512) void build_tiles_kernel(const int* __restrict_
         }
         seg[tid] = s0;
         if (tid == nseg - 1) seg[nseg] = s1;
-        nt = (s1 - s0 + tile_rows - 1) / tile_rows;
+        nt = seg_tiles(s1 - s0, tile_rows, fold);
     }
     sc[tid] = nt;
     __syncthreads();
@@ -1248,8 +1307,21 @@ int stream_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st,
 
 // LDS-tiled (prefill) form: one work-group per (256-row tile, column block of 128 (gate/up)
 // or 256 (down)); grid = 8 x per-XCD range, sized for the most tiles the batch can have.
+// fold: the tile table folds remainders (tile_fold), so the form with folded rows runs.
+template <int EPI, bool FOLD>
+int tile_launch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, const char* name);
+
 template <int EPI>
-int tile_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, const char* name) {
+int tile_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, const char* name,
+                  bool fold = false) {
+    if constexpr (EPI != EPI_F32) {  // the dense fp32-output form has no tile table
+        if (fold) return tile_launch<EPI, true>(wf, p, ntiles_max, st, name);
+    }
+    return tile_launch<EPI, false>(wf, p, ntiles_max, st, name);
+}
+
+template <int EPI, bool FOLD>
+int tile_launch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, const char* name) {
     const int cols = (EPI == EPI_SWIGLU) ? TBN / 2 : TBN;
     if (p.ncols % cols != 0 || p.K % TBK != 0) {
         set_error("%s: tiled form needs columns %% %d == 0 and K %% %d == 0", name, cols, TBK);
@@ -1266,15 +1338,22 @@ int tile_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, c
         gemm_tile_kernel<YVMOE_W_BF16, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb);
     } else {
         switch (wf) {
-            case YVMOE_W_BF16: gemm_tile_kernel<YVMOE_W_BF16, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
-            case YVMOE_W_INT8: gemm_tile_kernel<YVMOE_W_INT8, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
-            case YVMOE_W_FP8: gemm_tile_kernel<YVMOE_W_FP8, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
+            case YVMOE_W_BF16: gemm_tile_kernel<YVMOE_W_BF16, EPI, 8192, FOLD><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
+            case YVMOE_W_INT8: gemm_tile_kernel<YVMOE_W_INT8, EPI, 8192, FOLD><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
+            case YVMOE_W_FP8: gemm_tile_kernel<YVMOE_W_FP8, EPI, 8192, FOLD><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
             case YVMOE_W_INT4:
                 if (p.K > 8192) {  // the group-scale table in LDS holds K / 128 <= 64 groups
                     set_error("%s: tiled int4 form needs K <= 8192 (K=%d)", name, p.K);
                     return YVMOE_ERR_SHAPE;
                 }
-                gemm_tile_kernel<YVMOE_W_INT4, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb);
+                if constexpr (FOLD) {
+                    if (p.K <= 5120)  // 40 scale groups beside a 3-stage ring
+                        gemm_tile_kernel<YVMOE_W_INT4, EPI, 5120, true><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb);
+                    else              // 64 groups beside a 2-stage ring
+                        gemm_tile_kernel<YVMOE_W_INT4, EPI, 8192, true><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb);
+                } else {
+                    gemm_tile_kernel<YVMOE_W_INT4, EPI, 8192, false><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb);
+                }
                 break;
             default: set_error("%s: no tiled form for weight format %d", name, wf); return YVMOE_ERR_DTYPE;
         }
@@ -1447,6 +1526,7 @@ TileTable ffn_tile_table(int N, int k, int E, int S, int F, int act, int tile_ro
     t.ntiles = (int*)(fws + FL.ntiles);
     t.S = S;
     t.tile_rows = tile_rows;
+    t.fold = tile_rows == TBM ? tile_fold(N, k, E) : 0;
     return t;
 }
 
@@ -1467,8 +1547,8 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     int* ntiles = tt.ntiles;
     const int T = max_tiles(N, k, E, S, tile_rows);
     if (!tiles_ready) {
-        build_tiles_kernel<<<1, 512, 0, st>>>(routing->offsets, E, S, N, k, tile_rows, seg, tile_seg,
-                                              tile_row0, ntiles);
+        build_tiles_kernel<<<1, 512, 0, st>>>(routing->offsets, E, S, N, k, tile_rows, tt.fold, seg,
+                                              tile_seg, tile_row0, ntiles);
         YV_LAUNCH_CHECK("build_tiles");
     }
     const int wf = w->format;
@@ -1497,7 +1577,7 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.ldo = F;
     p.kchunk = H;
     const bool streaming = (maxrb == 1);
-    int rc = tiled ? tile_dispatch<EPI_SWIGLU>(wf, p, T, st, "expert_gemm1")
+    int rc = tiled ? tile_dispatch<EPI_SWIGLU>(wf, p, T, st, "expert_gemm1", tt.fold > 0)
            : streaming ? stream_dispatch<EPI_SWIGLU, 4, YV_NB1>(wf, p, T, st, "expert_gemm1")
                        : gemm_dispatch<EPI_SWIGLU>(act, wf, p, T, (F % 32 == 0) ? 2 : 1, 1, st,
                                                    "expert_gemm1", maxrb);
@@ -1519,7 +1599,7 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.out = y;
     p.ldo = H;
     p.kchunk = F;
-    if (tiled) return tile_dispatch<EPI_DOWN>(wf, p, T, st, "expert_gemm2");
+    if (tiled) return tile_dispatch<EPI_DOWN>(wf, p, T, st, "expert_gemm2", tt.fold > 0);
     return streaming ? stream_dispatch<EPI_DOWN, 4, YV_NB2>(wf, p, T, st, "expert_gemm2")
                      : gemm_dispatch<EPI_DOWN>(act, wf, p, T, (H % 32 == 0) ? 2 : 1, 1, st,
                                                "expert_gemm2", maxrb);

@@ -703,7 +703,7 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
     }
     if (wave == 15 && a.tiles.seg != nullptr) {
         // tile table of the expert GEMMs (build_tiles_kernel): lane l owns segments 5l .. 5l + 4
-        const int S = a.tiles.S, tr = a.tiles.tile_rows;
+        const int S = a.tiles.S, tr = a.tiles.tile_rows, fold = a.tiles.fold;
         const int nseg = E + S;
         int s0[5], nt[5], loc = 0;
 #pragma unroll
@@ -722,7 +722,7 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
                 if (sg == nseg - 1) a.tiles.seg[nseg] = e_;
             }
             s0[i] = b;
-            nt[i] = (e_ - b + tr - 1) / tr;
+            nt[i] = seg_tiles(e_ - b, tr, fold);
             loc += nt[i];
         }
         const int incl = wave_incl_scan(loc);

@@ -150,6 +150,32 @@ def test_bf16_tiled_prefill_shapes(cuda, oracle):
     _run_and_check(oracle, w)
 
 
+@pytest.mark.parametrize("fmt", ["int8", "int4", "fp8", "bf16"])
+def test_tiled_folded_remainders(cuda, oracle, fmt):
+    """Expert segments of 256, 257, 272, 273, 288, 289, 544 and 145 rows and a shared segment of
+    2324 rows (9 x 256 + 20), forced through one-hot gate rows: the LDS-tiled form folds a
+    remainder of 1 .. 32 rows into the segment's last full tile (a second launch runs those
+    tiles; 17+ rows reach the second wavefront row's block) and keeps 33 rows as a tile of
+    their own."""
+    from pisceslx_amd import _lib
+    from pisceslx_amd.workloads import LayerSpec
+    counts = [256, 257, 272, 273, 288, 289, 544, 145]
+    E, H, F, N = len(counts), 256, 256, sum(counts)
+    spec = LayerSpec("folds", H, F, E, 1, 1, getattr(_lib, "W_" + fmt.upper()), torch.bfloat16,
+                     fixed_shape_mode=True)
+    w = make_workload(spec, device="cuda", lengths=[N])
+    g = torch.Generator().manual_seed(5)
+    expert = torch.repeat_interleave(torch.arange(E), torch.tensor(counts))[torch.randperm(N, generator=g)]
+    x = torch.randn(N, H, generator=g) * 0.5
+    x[torch.arange(N), expert] += 8.0
+    gate = torch.zeros(E, H)
+    gate[torch.arange(E), torch.arange(E)] = 1.0
+    w.x = x.to(torch.bfloat16).cuda()
+    w.gate_weight = gate.to(torch.bfloat16).cuda()
+    _, _, routing = _run_and_check(oracle, w)
+    assert routing.counts.cpu().tolist() == counts
+
+
 def test_forward_is_deterministic(cuda, oracle):
     w = make_workload("cfg3", device="cuda", n_tokens=700)
     st = router_state(w)
