@@ -51,11 +51,19 @@ inline int router_ld(int E, int act) {
 // one work-group).
 constexpr int kSmallRouteTok = 256;
 
+#ifndef YV_ROUTER_KS_MAX
+// most router K splits: 16 measured best for 1-256 tokens at H = 4096, E = 64 (cfg2 decode
+// layer step 227 -> 224 us against 32 splits; 8 and 4 slower)
+#define YV_ROUTER_KS_MAX 16
+#endif
+
 inline int router_ksplit(int N, int E, int act, int H) {
     const int groups = ceil_div(router_ld(E, act), 64);
     const int wgs = ceil_div(N > 0 ? N : 1, 64) * groups;
     int ks = 1;
-    while (wgs * ks * 2 <= 512 && H % (ks * 2 * 64) == 0 && H / (ks * 2) >= 128) ks *= 2;
+    while (ks * 2 <= YV_ROUTER_KS_MAX && wgs * ks * 2 <= 512 && H % (ks * 2 * 64) == 0 &&
+           H / (ks * 2) >= 128)
+        ks *= 2;
     return ks;
 }
 
