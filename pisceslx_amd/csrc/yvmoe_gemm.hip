@@ -1194,9 +1194,16 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
         acc[v] = 0.0f;
         sh[v] = 0.0f;
     }
-    auto load = [&](long long row, float* dst) {
+    // Rows are loaded KC at a time, all in flight together, then summed in slot order: the
+    // arithmetic is the same as a load-then-add loop, without one memory round trip per slot.
+    constexpr int KC = 8;
+    typedef typename std::conditional<ACT == YVMOE_ACT_BF16, uint4, float4>::type Raw;
+    auto raw_load = [&](long long row) -> Raw {
+        if constexpr (ACT == YVMOE_ACT_BF16) return *(const uint4*)((const unsigned short*)y + row * H + h);
+        else return *(const float4*)((const float*)y + row * H + h);
+    };
+    auto unpack = [&](const Raw& q, float* dst) {
         if constexpr (ACT == YVMOE_ACT_BF16) {
-            const uint4 q = *(const uint4*)((const unsigned short*)y + row * H + h);
             const unsigned u[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -1204,7 +1211,6 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
                 dst[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
             }
         } else {
-            const float4 q = *(const float4*)((const float*)y + row * H + h);
             dst[0] = q.x;
             dst[1] = q.y;
             dst[2] = q.z;
@@ -1212,17 +1218,40 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
         }
     };
     float tmp[VEC];
-    for (int j = 0; j < k; ++j) {
-        const float wj = w[(long long)t * k + j];
-        load(pos[(long long)t * k + j], tmp);
+    for (int j0 = 0; j0 < k; j0 += KC) {
+        float wj[KC];
+        Raw q[KC];
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) acc[v] = acc[v] + wj * tmp[v];
+        for (int i = 0; i < KC; ++i) {
+            if (j0 + i < k) {
+                const long long sl = (long long)t * k + j0 + i;
+                wj[i] = w[sl];
+                q[i] = raw_load(pos[sl]);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < KC; ++i) {
+            if (j0 + i < k) {
+                unpack(q[i], tmp);
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) acc[v] = acc[v] + wj[i] * tmp[v];
+            }
+        }
     }
-    for (int s = 0; s < S; ++s) {
-        const float ms = mix[s];
-        load((long long)N * k + (long long)s * N + t, tmp);
+    for (int s0 = 0; s0 < S; s0 += KC) {
+        Raw q[KC];
 #pragma unroll
-        for (int v = 0; v < VEC; ++v) sh[v] = rnd<ACT>(sh[v] + rnd<ACT>(ms * tmp[v]));
+        for (int i = 0; i < KC; ++i)
+            if (s0 + i < S) q[i] = raw_load((long long)N * k + (long long)(s0 + i) * N + t);
+#pragma unroll
+        for (int i = 0; i < KC; ++i) {
+            if (s0 + i < S) {
+                const float ms = mix[s0 + i];
+                unpack(q[i], tmp);
+#pragma unroll
+                for (int v = 0; v < VEC; ++v) sh[v] = rnd<ACT>(sh[v] + rnd<ACT>(ms * tmp[v]));
+            }
+        }
     }
     // routed output rounded to the layer dtype, shared mixture and residual sums rounded
     // after every step, as the reference's tensors of that dtype are (layer.py:859-863,
