@@ -741,6 +741,7 @@ template <int WF, int EPI, int S4K = 8192, bool FOLD = false>
 __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int ncb) {
     typedef TileCfg<WF, S4K, FOLD> C;
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
+    constexpr bool WFIRST = WF != YVMOE_W_BF16;  // weights as the MFMA's first operand
     constexpr bool GROUPED = WF == YVMOE_W_FP8;
     constexpr long long B_CHUNK = C::B_BLK;  // bytes of a weight block (64-wide K step)
     __shared__ __attribute__((aligned(1024))) unsigned char lds_a[C::NST][C::A_BYTES];
@@ -817,20 +818,27 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
             b_dst[j] = C::I4 ? rb * 512 + half * 256 : blk * 1024;
         }
 
-        // The weights are the MFMA's first operand: lane l supplies weight row brow[nb] as operand
-        // row i = l % 16 of fragment nb, and its accumulator ends with output row c = l % 16 of
-        // the row block and the columns of operand rows 4 (l / 16) .. + 3. Gate/up: fragment nb
-        // is rows wc 16 + i of the gate (0) or up (1) half, so a lane holds gate and up of the same
-        // 4 columns. Down / fp32 output: the wavefront's 32 rows are dealt out in groups of four,
-        // group q = i / 4 of fragment nb taking rows 8 q + 4 ((q / 2) ^ nb) + i % 4, so that lane l
-        // holds the 8 consecutive columns 8 (l / 16) .. + 7 (fragment 0 first for l < 32) and the
-        // epilogue writes 16 bytes per lane; the LDS reads of a fragment still cover 16 distinct
-        // 16-byte bank groups per 16 lanes.
+        // Quantized weights (WFIRST) are the MFMA's first operand: lane l supplies weight row
+        // brow[nb] as operand row i = l % 16 of fragment nb, and its accumulator ends with output
+        // row c = l % 16 of the row block and the columns of operand rows 4 (l / 16) .. + 3.
+        // Gate/up: fragment nb is rows wc 16 + i of the gate (0) or up (1) half, so a lane holds
+        // gate and up of the same 4 columns. Down: the wavefront's 32 rows are dealt out in
+        // groups of four, group q = i / 4 of fragment nb taking rows 8 q + 4 ((q / 2) ^ nb) + i % 4,
+        // so that lane l holds the 8 consecutive columns 8 (l / 16) .. + 7 (fragment 0 first for
+        // l < 32) and the epilogue writes 16 bytes per lane; the LDS reads of a fragment still
+        // cover 16 distinct 16-byte bank groups per 16 lanes.
+        // bf16 weights (and so the fp32-output form) are the second operand (fragment nb = rows
+        // 16 nb + i; gate/up as above): back-to-back MFMAs then share their first operand (the
+        // activation fragment), which measured 16-25 % faster where no dequantization runs
+        // between them (same results); the accumulator holds rows 4 (l / 16) .. + 3 and column
+        // l % 16, stored element by element.
         int brow[2];
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
             const int i = lane & 15, q = i >> 2;
-            brow[nb] = SWIGLU ? nb * (TBN / 2) + wc * 16 + i : wc * 32 + q * 8 + 4 * ((q >> 1) ^ nb) + (i & 3);
+            if constexpr (SWIGLU) brow[nb] = nb * (TBN / 2) + wc * 16 + i;
+            else if constexpr (!WFIRST) brow[nb] = wc * 32 + nb * 16 + i;
+            else brow[nb] = wc * 32 + q * 8 + 4 * ((q >> 1) ^ nb) + (i & 3);
         }
         float cs[2] = {1.0f, 1.0f};  // int8: per-column scales
         int sblk[2] = {0, 0};        // fp8: which of the tile's two scale blocks
@@ -960,8 +968,13 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
                     const bf16x8 a1 = *(const bf16x8*)(As + a_rd1 + mb * 16 * 128);
 #pragma unroll
                     for (int nb = 0; nb < 2; ++nb) {
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][0], a0, acc[mb][nb], 0, 0, 0);
-                        acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][1], a1, acc[mb][nb], 0, 0, 0);
+                        if constexpr (WFIRST) {
+                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][0], a0, acc[mb][nb], 0, 0, 0);
+                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][1], a1, acc[mb][nb], 0, 0, 0);
+                        } else {
+                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bq[nb][0], acc[mb][nb], 0, 0, 0);
+                            acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bq[nb][1], acc[mb][nb], 0, 0, 0);
+                        }
                     }
                 }
                 if constexpr (EXT) {
@@ -969,8 +982,13 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
                     const bf16x8 a1 = *(const bf16x8*)(As + xa_rd1);
 #pragma unroll
                     for (int nb = 0; nb < 2; ++nb) {
-                        accx[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][0], a0, accx[nb], 0, 0, 0);
-                        accx[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][1], a1, accx[nb], 0, 0, 0);
+                        if constexpr (WFIRST) {
+                            accx[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][0], a0, accx[nb], 0, 0, 0);
+                            accx[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bq[nb][1], a1, accx[nb], 0, 0, 0);
+                        } else {
+                            accx[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, bq[nb][0], accx[nb], 0, 0, 0);
+                            accx[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, bq[nb][1], accx[nb], 0, 0, 0);
+                        }
                     }
                 }
             };
@@ -983,7 +1001,35 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
 
         // epilogue: row l % 16 of each 16-row block; gate/up 4 consecutive columns (8-byte
         // stores), down 8 (16-byte stores)
-        auto store = [&](int r, f32x4 c0, f32x4 c1) {
+        // one 16-row block at row rb: WFIRST, lane row rb + l % 16; else rows rb + 4 (l / 16) + i
+        auto store_block = [&](int rb, f32x4 c0, f32x4 c1) {
+            if constexpr (!WFIRST) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = rb + 4 * g + i;
+                    if (r >= seg_end) continue;
+                    if constexpr (SWIGLU) {
+                        const int n = n0 + wc * 16 + (lane & 15);
+                        const float gt = round_bf16(c0[i]);
+                        const float up = round_bf16(c1[i]);
+                        ((unsigned short*)p.out)[(long long)r * p.ldo + n] =
+                            f32_to_bf16_rne(round_bf16(silu(gt)) * up);
+                    } else {
+#pragma unroll
+                        for (int nb = 0; nb < 2; ++nb) {
+                            const int n = n0 + wc * 32 + nb * 16 + (lane & 15);
+                            const float v = nb ? c1[i] : c0[i];
+                            if constexpr (EPI == EPI_F32)
+                                ((float*)p.out)[(long long)r * p.ldo + n] = f32_out(p, v, n, 0);
+                            else
+                                ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(v);
+                        }
+                    }
+                }
+                return;
+            }
+            const int r = rb + (lane & 15);
+            if (r >= seg_end) return;
             if constexpr (SWIGLU) {
                 const int n = n0 + wc * 16 + 4 * g;
                 float hv[4];
@@ -999,29 +1045,14 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
                 const int n = n0 + wc * 32 + 8 * g;
                 const f32x4 lo = g < 2 ? c0 : c1;
                 const f32x4 hi = g < 2 ? c1 : c0;
-                if constexpr (EPI == EPI_F32) {
-                    float* o = (float*)p.out + (long long)r * p.ldo + n;
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        o[i] = f32_out(p, lo[i], n + i, 0);
-                        o[4 + i] = f32_out(p, hi[i], n + 4 + i, 0);
-                    }
-                } else {
-                    *(uint4*)((unsigned short*)p.out + (long long)r * p.ldo + n) =
-                        make_uint4(pack_bf16(lo[0], lo[1]), pack_bf16(lo[2], lo[3]),
-                                   pack_bf16(hi[0], hi[1]), pack_bf16(hi[2], hi[3]));
-                }
+                *(uint4*)((unsigned short*)p.out + (long long)r * p.ldo + n) =
+                    make_uint4(pack_bf16(lo[0], lo[1]), pack_bf16(lo[2], lo[3]),
+                               pack_bf16(hi[0], hi[1]), pack_bf16(hi[2], hi[3]));
             }
         };
 #pragma unroll
-        for (int mb = 0; mb < 8; ++mb) {
-            const int r = row0 + wr * 128 + mb * 16 + (lane & 15);
-            if (r < seg_end) store(r, acc[mb][0], acc[mb][1]);
-        }
-        if (xlive) {
-            const int r = row0 + TBM + wr * 16 + (lane & 15);
-            if (r < seg_end) store(r, accx[0], accx[1]);
-        }
+        for (int mb = 0; mb < 8; ++mb) store_block(row0 + wr * 128 + mb * 16, acc[mb][0], acc[mb][1]);
+        if (xlive) store_block(row0 + TBM + wr * 16, accx[0], accx[1]);
     };
     if (FOLD && ext > 0 && ext <= kTileFold) run_tile(std::integral_constant<bool, FOLD>{});
     else run_tile(std::false_type{});
