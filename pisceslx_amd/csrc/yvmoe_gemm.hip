@@ -1229,9 +1229,14 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
     // arithmetic is the same as a load-then-add loop, without one memory round trip per slot.
     constexpr int KC = 8;
     typedef typename std::conditional<ACT == YVMOE_ACT_BF16, uint4, float4>::type Raw;
+    // every expert-output row is read by exactly one token: non-temporal loads
     auto raw_load = [&](long long row) -> Raw {
-        if constexpr (ACT == YVMOE_ACT_BF16) return *(const uint4*)((const unsigned short*)y + row * H + h);
-        else return *(const float4*)((const float*)y + row * H + h);
+        if constexpr (ACT == YVMOE_ACT_BF16) {
+            return nt_load16((const char*)((const unsigned short*)y + row * H + h));
+        } else {
+            const u32x4 v = __builtin_nontemporal_load((const u32x4*)((const float*)y + row * H + h));
+            return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+        }
     };
     auto unpack = [&](const Raw& q, float* dst) {
         if constexpr (ACT == YVMOE_ACT_BF16) {
