@@ -1561,7 +1561,12 @@ int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, flo
     }
     p.out = partials;
     p.split_stride = (long long)N * ld;
-    int rc = gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), 1, ks, st, "router_gemm");
+    int rc;
+    if (dense_streamed(act, N, p.ncols, r->hidden))  // up to 64 rows: the weight-streaming form
+        rc = N <= 16 ? stream_dispatch<EPI_F32, 4, 1, 1>(YVMOE_W_BF16, p, 1, st, "router_gemm", ks)
+                     : stream_dispatch<EPI_F32, 2, 1, 4>(YVMOE_W_BF16, p, 1, st, "router_gemm", ks);
+    else
+        rc = gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), 1, ks, st, "router_gemm");
     if (rc || !reduce) return rc;
     const long long n = (long long)N * ld;
     reduce_splits_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(partials, ks, n, n, out);
