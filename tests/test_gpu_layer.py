@@ -150,17 +150,19 @@ def test_bf16_tiled_prefill_shapes(cuda, oracle):
     _run_and_check(oracle, w)
 
 
-@pytest.mark.parametrize("fmt", ["int8", "int4", "fp8", "bf16"])
-def test_tiled_folded_remainders(cuda, oracle, fmt):
+@pytest.mark.parametrize("fmt,hidden", [("int8", 256), ("int4", 256), ("fp8", 256), ("bf16", 256),
+                                        ("int4", 6144)])
+def test_tiled_folded_remainders(cuda, oracle, fmt, hidden):
     """Expert segments of 256, 257, 272, 273, 288, 289, 544 and 145 rows and a shared segment of
     2324 rows (9 x 256 + 20), forced through one-hot gate rows: the LDS-tiled form folds a
     remainder of 1 .. 32 rows into the segment's last full tile (a second launch runs those
     tiles; 17+ rows reach the second wavefront row's block) and keeps 33 rows as a tile of
-    their own."""
+    their own. int4 at hidden 6144 takes the gate/up form for K > 5120 (2-stage ring beside the
+    64-group scale table)."""
     from pisceslx_amd import _lib
     from pisceslx_amd.workloads import LayerSpec
     counts = [256, 257, 272, 273, 288, 289, 544, 145]
-    E, H, F, N = len(counts), 256, 256, sum(counts)
+    E, H, F, N = len(counts), hidden, 256, sum(counts)
     spec = LayerSpec("folds", H, F, E, 1, 1, getattr(_lib, "W_" + fmt.upper()), torch.bfloat16,
                      fixed_shape_mode=True)
     w = make_workload(spec, device="cuda", lengths=[N])
