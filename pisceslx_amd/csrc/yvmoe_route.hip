@@ -463,7 +463,7 @@ __global__ __launch_bounds__(256) void renorm_kernel(const float* __restrict__ w
 // ------------------------------------------------------------------ small batches
 // Routing of a batch of up to kSmallRouteTok tokens (decode) in two launches.
 //
-// route_topk_small_kernel: 4 tokens per work-group (16 lanes each). The token's logits and
+// route_topk_small_kernel: one token per work-group of 256 threads. The token's logits and
 // predictor columns are first summed over the router GEMM's K splits, in split order (the
 // order of reduce_splits_kernel), into LDS with all loads in flight; then the per-token
 // top-k and predictor run from LDS (topk_token, predictor_token: the same code as the
