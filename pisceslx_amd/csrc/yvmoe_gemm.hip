@@ -1562,9 +1562,11 @@ int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, flo
     p.out = partials;
     p.split_stride = (long long)N * ld;
     int rc;
-    if (dense_streamed(act, N, p.ncols, r->hidden))  // up to 64 rows: the weight-streaming form
-        rc = N <= 16 ? stream_dispatch<EPI_F32, 4, 1, 1>(YVMOE_W_BF16, p, 1, st, "router_gemm", ks)
-                     : stream_dispatch<EPI_F32, 2, 1, 4>(YVMOE_W_BF16, p, 1, st, "router_gemm", ks);
+    // up to 64 rows: the weight-streaming form, in 16-row tiles (the router operand, 2 MB at
+    // E = 64, stays in L2 for the tiles that re-read it: 2.7 us less per decode step than one
+    // 64-row tile; the 138 MB YvMoEGate projection keeps 64-row tiles, which measured faster)
+    if (dense_streamed(act, N, p.ncols, r->hidden))
+        rc = stream_dispatch<EPI_F32, 4, 1, 1>(YVMOE_W_BF16, p, ceil_div(N, 16), st, "router_gemm", ks);
     else
         rc = gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), 1, ks, st, "router_gemm");
     if (rc || !reduce) return rc;
