@@ -190,16 +190,21 @@ struct BLoad<YVMOE_W_INT4> {
     static __device__ __forceinline__ void load_blk_nt(Raw& r, const char* p, int ks) {
         r = nt_load8(p + (size_t)ks * BLK);
     }
+    // q - 8 for a nibble q: one byte permute places q in the low mantissa bits of 2^23 (bit
+    // pattern 0x4B00000q is the float 2^23 + q), and subtracting 2^23 + 8 leaves q - 8; both
+    // steps are exact, so the value equals the integer conversion it replaces
     static __device__ __forceinline__ void cvt(const Raw& r, float s, Frag16& f) {
         const unsigned w[2] = {r.x, r.y};
         unsigned o[8];
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
+            const unsigned lo4 = w[i] & 0x0F0F0F0Fu;         // low nibbles (even k) of bytes 0..3
+            const unsigned hi4 = (w[i] >> 4) & 0x0F0F0F0Fu;  // high nibbles (odd k)
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const unsigned byte = (w[i] >> (8 * j)) & 0xffu;  // low nibble = even k
-                const float lo = (float)((int)(byte & 0xfu) - 8);
-                const float hi = (float)((int)(byte >> 4) - 8);
+                const unsigned sel = 0x070C0C00u | (unsigned)j;  // bytes: nibble j, 0, 0, 0x4B
+                const float lo = __uint_as_float(__builtin_amdgcn_perm(0x4B000000u, lo4, sel)) - 8388616.0f;
+                const float hi = __uint_as_float(__builtin_amdgcn_perm(0x4B000000u, hi4, sel)) - 8388616.0f;
                 o[4 * i + j] = pack_bf16(lo * s, hi * s);
             }
         }
