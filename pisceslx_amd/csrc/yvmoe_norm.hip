@@ -6,7 +6,7 @@
 // division (the product is within one fp32 ulp of the quotient), which keeps the kernel at
 // the HBM bound instead of the VALU bound of one IEEE division per element.
 //
-// One wavefront per row (four for batches under 2048 rows): 16-byte loads (8 bf16 / 4 fp32 per
+// Two wavefronts per row (four for batches under 2048 rows): 16-byte loads (8 bf16 / 4 fp32 per
 // lane per step), the sum of squares in lane order then a DPP row-rotation reduction, the four
 // DPP rows in order and the row's wavefronts in order, the row kept in registers between the
 // passes (H <= 8192 bf16 / 4096 fp32; longer rows are read again). Two norms in sequence (the MoE input of YvHybridBlock is norm_mlp(norm_fusion(h)),
@@ -45,7 +45,8 @@ __device__ __forceinline__ unsigned pack_bf16(float lo, float hi) {
 
 // ACT: activation dtype; NN: RMSNorms applied in sequence (1 or 2), each rounded to ACT before
 // the next one reads it, as two YvRMSNorm modules called one after the other round; WPR:
-// wavefronts per row (1, or 4 for small batches so that the 256 CUs have rows to work on).
+// wavefronts per row (2: half a row's registers per wavefront, 60 → 49 us at 16,721 rows
+// against 1; 4 for small batches so that the 256 CUs have rows to work on; 1 is supported).
 // Thread r of a row (r < 64 WPR) owns the 16-byte chunks c = r + 64 WPR i.
 template <int ACT, int NN, int WPR>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, NormChain nc, int N, int H,
@@ -53,10 +54,16 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, NormChain n
     constexpr int EPC = ACT == YVMOE_ACT_BF16 ? 8 : 4;  // elements per 16-byte chunk
     constexpr int TPR = 64 * WPR;                       // threads per row
     constexpr int MAXC = 16 / WPR;                      // chunks per thread held in registers
-    __shared__ float s_part[NN][4];
+    constexpr int RPB = 256 / TPR;  // rows per work-group
+    __shared__ float s_part[RPB][NN][4];
     const int r = threadIdx.x % TPR;
-    const int row = blockIdx.x * (256 / TPR) + threadIdx.x / TPR;
-    if (row >= N) return;  // WPR = 4: the whole block leaves together
+    const int slot = threadIdx.x / TPR;
+    const int row_id = blockIdx.x * RPB + slot;
+    if (WPR == 1 && row_id >= N) return;  // no barrier in a one-wavefront row
+    // several wavefronts per row share barriers: a row past N computes on a copy of the last
+    // row and stores nothing
+    const bool live = row_id < N;
+    const int row = live ? row_id : N - 1;
     const int nch = H / EPC;  // H % EPC == 0 (checked on the host)
     const size_t rb = (size_t)row * H * (ACT == YVMOE_ACT_BF16 ? 2 : 4);
     const u32x4n* xr = (const u32x4n*)((const char*)x + rb);
@@ -105,11 +112,11 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, NormChain n
     auto rinv_of = [&](float acc, int n) {
         float tot = wave_sum_n(acc);
         if (WPR > 1) {
-            if ((threadIdx.x & 63) == 0) s_part[n][r >> 6] = tot;
+            if ((threadIdx.x & 63) == 0) s_part[slot][n][r >> 6] = tot;
             __syncthreads();
-            tot = s_part[n][0];
+            tot = s_part[slot][n][0];
 #pragma unroll
-            for (int w = 1; w < WPR; ++w) tot += s_part[n][w];
+            for (int w = 1; w < WPR; ++w) tot += s_part[slot][n][w];
         }
         return 1.0f / sqrtf(tot / (float)H + nc.eps[n]);
     };
@@ -142,7 +149,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, NormChain n
 #pragma unroll
         for (int i = 0; i < MAXC; ++i) {
             const int c = r + TPR * i;
-            if (c < nch) yr[c] = norm_chunk(v[i], c, rinv, NN - 1);
+            if (live && c < nch) yr[c] = norm_chunk(v[i], c, rinv, NN - 1);
         }
     } else {
         // long rows: the intermediate norm goes through y (each thread re-reads only the
@@ -155,13 +162,14 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, NormChain n
             acc = 0.f;
             for (int c = r; c < nch; c += TPR) {
                 const u32x4n o = norm_chunk(src[c], c, rinv, n);
-                yr[c] = o;
+                if (live) yr[c] = o;
                 acc += sumsq(o);
             }
             src = yr;
         }
         const float rinv = rinv_of(acc, NN - 1);
-        for (int c = r; c < nch; c += TPR) yr[c] = norm_chunk(src[c], c, rinv, NN - 1);
+        if (live)
+            for (int c = r; c < nch; c += TPR) yr[c] = norm_chunk(src[c], c, rinv, NN - 1);
     }
 }
 
@@ -169,9 +177,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const void* x, NormChain n
 
 template <int ACT, int NN>
 void rmsnorm_dispatch(const void* x, const NormChain& nc, int N, int H, void* y, hipStream_t st) {
-    // a wavefront per row once the rows fill the chip; four per row below that
+    // two wavefronts per row once the rows fill the chip; four per row below that
     if (N >= 2048)
-        rmsnorm_kernel<ACT, NN, 1><<<(unsigned)((N + 3) / 4), 256, 0, st>>>(x, nc, N, H, y);
+        rmsnorm_kernel<ACT, NN, 2><<<(unsigned)((N + 1) / 2), 256, 0, st>>>(x, nc, N, H, y);
     else
         rmsnorm_kernel<ACT, NN, 4><<<(unsigned)N, 256, 0, st>>>(x, nc, N, H, y);
 }

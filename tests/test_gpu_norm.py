@@ -97,11 +97,13 @@ def _compare(got, want, norms, x):
     (50, 4096, torch.float32, 2, True),
     (4, 8192, torch.float32, 2, False),
     (1, 24, torch.float32, 1, False),
-    # 2048 rows and more: one wavefront per row instead of four
+    # 2048 rows and more: two wavefronts per row instead of four
     (2100, 4096, torch.bfloat16, 2, False),
     (2048, 5120, torch.bfloat16, 1, True),
     (2050, 12288, torch.bfloat16, 2, True),
     (2049, 2048, torch.float32, 2, True),
+    (2049, 4096, torch.bfloat16, 2, False),   # odd count: the last work-group has a dead row
+    (2051, 16384, torch.bfloat16, 2, True),   # the same, rows longer than the registers hold
 ])
 def test_rmsnorm_matches_oracle(cuda, N, H, dtype, nn, bias):
     print(f"rmsnorm N={N} H={H} dtype={dtype} norms={nn} bias={bias}", flush=True)
