@@ -692,15 +692,17 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef __attribute__((address_space(1))) void* gbl_ptr_t;
 
 // Direct-to-LDS load of 16 bytes per lane: lane L's bytes land at dst + 16 L (dst is the
-// same for the whole wavefront and goes to M0).
+// same for the whole wavefront). The LDS base travels in M0, which the instruction reads:
+// it is an input operand of the asm bound to M0 ("{m0}"), so the compiler writes M0 itself
+// and knows its value, and the asm modifies no register the compiler reserves.
 __device__ __forceinline__ void dma16(const void* src, void* dst) {
     const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_ptr_t)dst);
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" : : "s"(m0), "v"(src) : "memory", "m0");
+    asm volatile("global_load_lds_dwordx4 %0, off" : : "v"(src), "{m0}"(m0) : "memory");
 }
 // The same with 4 bytes per lane (256 B per wavefront at dst + 4 L).
 __device__ __forceinline__ void dma4(const void* src, void* dst) {
     const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)(lds_ptr_t)dst);
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" : : "s"(m0), "v"(src) : "memory", "m0");
+    asm volatile("global_load_lds_dword %0, off" : : "v"(src), "{m0}"(m0) : "memory");
 }
 
 __device__ __forceinline__ int swz_a(int r, int c) {  // bytes, 128-byte rows

@@ -477,7 +477,6 @@ __global__ __launch_bounds__(256) void renorm_kernel(const float* __restrict__ w
 // capacity_trim_kernel (p > T, then the first ties in token order).
 constexpr int kSmallSlots = kSmallRouteTok * YVMOE_MAX_TOPK;
 constexpr int kSmallChunks = kSmallSlots / 64;
-constexpr int kSmallBlocks = kSmallRouteTok / kTokPerBlock;
 constexpr int kMaxPredTerms = 3;  // predictor columns per hidden unit held in LDS
 
 // One token per work-group of 256 threads: each thread reduces about one column over the K
