@@ -216,6 +216,24 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
                       void* stream);
 
 /*
+ * yvmoe_forward with no workspace argument: the whole layer on a scratch buffer the library
+ * holds itself, so the call allocates nothing (no hipMalloc / hipFree, no allocating library
+ * routine). This entry point has no counterpart in the reference; it is for callers that
+ * cannot allocate device memory: code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc. The caller still passes x, out, shared_out and the routing buffers.
+ * The scratch is one device array of YVMOE_STATIC_SCRATCH_BYTES per GPU, held from the first
+ * call on that GPU until the process ends; a call whose yvmoe_workspace_bytes() exceeds it
+ * returns YVMOE_ERR_WORKSPACE (at cfg2's shape, hidden 4096 / 64 experts / top-6 / 2 shared,
+ * up to 689 tokens fit). Every call on one GPU shares that GPU's scratch, which keeps the last
+ * call's contents: calls that overlap on one GPU (other streams, other host threads) race.
+ */
+#define YVMOE_STATIC_SCRATCH_BYTES (64u << 20)
+int32_t yvmoe_forward_static(const void* x, int32_t act_dtype, int32_t n_tokens,
+                             const yvmoe_router* router, const yvmoe_expert_weights* experts,
+                             const float* mix, const void* skip, void* out, void* shared_out,
+                             yvmoe_routing* routing, void* stream);
+
+/*
  * YvMoEGate (model/moe/gate.py:140-451), the router the reference's MoE layers build
  * (model/moe/layer.py:754-777). Weights as the module holds them, regrouped once:
  *   w_proj [P][H] (activation dtype), the projections of x in one matrix: with the HiCL head,

@@ -35,6 +35,7 @@ MAX_EXPERTS = 256
 MAX_TOPK = 16
 MAX_SHARED = 8
 PREDICTOR_DIM = 64
+STATIC_SCRATCH_BYTES = 64 << 20
 
 EXPORTED_SYMBOLS = (
     "yvmoe_last_error",
@@ -46,6 +47,7 @@ EXPORTED_SYMBOLS = (
     "yvmoe_expert_ffn",
     "yvmoe_combine",
     "yvmoe_forward",
+    "yvmoe_forward_static",
     "yvmoe_moegate_workspace_bytes",
     "yvmoe_moegate_logits",
     "yvmoe_moegate_forward_workspace_bytes",
@@ -190,6 +192,10 @@ def _declare(l: ctypes.CDLL) -> None:
                                         ctypes.POINTER(Routing), vp, vp, vp, sz, vp]
     l.yvmoe_rmsnorm.restype = i32
     l.yvmoe_rmsnorm.argtypes = [vp, i32, i32, i32, ctypes.POINTER(RMSNormParams), i32, vp, vp]
+    l.yvmoe_forward_static.restype = i32
+    l.yvmoe_forward_static.argtypes = [vp, i32, i32, ctypes.POINTER(Router),
+                                       ctypes.POINTER(ExpertWeights), vp, vp, vp, vp,
+                                       ctypes.POINTER(Routing), vp]
     l.yvmoe_forward.restype = i32
     l.yvmoe_forward.argtypes = [vp, i32, i32, ctypes.POINTER(Router), ctypes.POINTER(ExpertWeights),
                                 vp, vp, vp, vp, ctypes.POINTER(Routing), vp, sz, vp]

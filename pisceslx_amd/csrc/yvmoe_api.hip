@@ -3,6 +3,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "yvmoe_internal.h"
 
 namespace yvmoe {
@@ -257,6 +259,64 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
     if (rc) return rc;
     return combine_launch(y, act_dtype, N, experts->hidden, k, experts->num_shared, routing, mix,
                           skip, out, shared_out, st);
+}
+
+}  // extern "C"
+
+namespace yvmoe {
+
+// Scratch of yvmoe_forward_static: one file-scope device array, which every GPU the library
+// runs on holds (its own copy at its own address) until the process ends. In host code the
+// array's name is a host-side stand-in, not a device address: the kernels get the address
+// hipGetSymbolAddress returns for the current device, looked up once per device.
+static __device__ __align__(256) unsigned char scratch[YVMOE_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices] = {};
+
+static int static_scratch(void** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    YV_REQUIRE(e == hipSuccess && dev >= 0 && dev < kMaxDevices, YVMOE_ERR_LAUNCH,
+               "hipGetDevice failed (%s) or device %d beyond %d", hipGetErrorString(e), dev,
+               kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        YV_REQUIRE(e == hipSuccess && p != nullptr, YVMOE_ERR_LAUNCH,
+                   "hipGetSymbolAddress(scratch) on device %d failed: %s", dev, hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return YVMOE_OK;
+}
+
+}  // namespace yvmoe
+
+extern "C" {
+
+int32_t yvmoe_forward_static(const void* x, int32_t act_dtype, int32_t n_tokens,
+                             const yvmoe_router* router, const yvmoe_expert_weights* experts,
+                             const float* mix, const void* skip, void* out, void* shared_out,
+                             yvmoe_routing* routing, void* stream) {
+    clear_error();
+    int rc = check_router(router, act_dtype);
+    if (rc) return rc;
+    rc = check_experts(experts, act_dtype);
+    if (rc) return rc;
+    YV_REQUIRE(n_tokens >= 0, YVMOE_ERR_ARG, "n_tokens=%d < 0", n_tokens);
+    const size_t need = yvmoe_workspace_bytes(n_tokens, act_dtype, router, experts);
+    YV_REQUIRE(need <= (size_t)YVMOE_STATIC_SCRATCH_BYTES, YVMOE_ERR_WORKSPACE,
+               "n_tokens=%d needs %zu bytes of scratch, more than the static %zu bytes of "
+               "yvmoe_forward_static (use yvmoe_forward with a workspace)",
+               n_tokens, need, (size_t)YVMOE_STATIC_SCRATCH_BYTES);
+    void* ws = nullptr;
+    rc = static_scratch(&ws);
+    if (rc) return rc;
+    return yvmoe_forward(x, act_dtype, n_tokens, router, experts, mix, skip, out, shared_out,
+                         routing, ws, (size_t)YVMOE_STATIC_SCRATCH_BYTES, stream);
 }
 
 static int check_moegate(const yvmoe_moegate* g, int act) {

@@ -198,6 +198,46 @@ def moe_forward(x2d: torch.Tensor, router: RouterState, experts: PackedExperts,
     return out, shared_out, routing
 
 
+def moe_forward_static(x2d: torch.Tensor, router: RouterState, experts: PackedExperts,
+                       mix: Optional[torch.Tensor], skip: Optional[torch.Tensor],
+                       out: Optional[torch.Tensor] = None,
+                       shared_out: Optional[torch.Tensor] = None,
+                       routing: Optional[Routing] = None):
+    """Whole layer on the library's own static scratch (yvmoe_forward_static): the library
+    call allocates no device memory. Pass ``out``, ``shared_out`` and ``routing`` to make the
+    whole call allocation-free (otherwise they are allocated here, before the library call).
+    Calls that overlap on one GPU share its scratch and race. Returns (out, shared_out or
+    None, Routing)."""
+    dev = _require_cuda(x2d, router.w_router, mix, skip, out, shared_out, *experts.tensors())
+    act = _act(x2d.dtype)
+    N, H = x2d.shape
+    if H != experts.hidden or H != router.hidden:
+        raise ValueError(f"hidden size {H} does not match the layer ({experts.hidden})")
+    E, k, S = router.num_experts, router.top_k, experts.num_shared
+    if skip is not None and (skip.shape != x2d.shape or skip.dtype != x2d.dtype):
+        raise ValueError("skip buffer must match x")
+    if mix is not None and (mix.dtype != torch.float32 or mix.numel() != S):
+        raise ValueError("mix must be fp32 [S]")
+    if routing is None:
+        routing = Routing.empty(N, E, k, dev)
+    if out is None:
+        out = torch.empty_like(x2d)
+    if shared_out is None and S > 0:
+        shared_out = torch.empty_like(x2d)
+    for t in (out, shared_out):
+        if t is not None and (t.shape != x2d.shape or t.dtype != x2d.dtype):
+            raise ValueError("out and shared_out must match x")
+    r = router.struct()
+    e = experts.struct()
+    o = routing.struct()
+    _lib.check(_lib.lib().yvmoe_forward_static(x2d.data_ptr(), act, N, ctypes.byref(r),
+                                                ctypes.byref(e), _ptr(mix), _ptr(skip),
+                                                out.data_ptr(), _ptr(shared_out) if S > 0 else None,
+                                                ctypes.byref(o), _stream(dev)),
+               "yvmoe_forward_static")
+    return out, (shared_out if S > 0 else None), routing
+
+
 @dataclass
 class MoEGateState:
     """Device tensors and constants of one YvMoEGate, regrouped for yvmoe_moegate_logits."""
