@@ -21,6 +21,9 @@
  *                           model/moe/expert.py:475-489, and the shared experts of
  *                           YvDynamicMoELayer._compute_shared_expert_output
  *                           model/moe/layer.py:812-865
+ *   yvmoe_dispatch       -> PiscesLxFusedMoEDispatch.forward opss/infer/fused_moe.py:54-123
+ *                           and PiscesLxFusedMoe.fused_moe_dispatch :129-143 (external
+ *                           routing weights and expert indices, routed experts, combine)
  *   yvmoe_combine        -> the index_add_ combine opss/infer/fused_moe.py:117-119, the
  *                           routed + shared sum model/moe/layer.py:942-945 and
  *                           _apply_skip_residual model/moe/layer.py:741-753
@@ -191,11 +194,37 @@ int32_t yvmoe_route(const float* logits, int32_t ld, const float* predictor, int
  * Grouped SwiGLU FFN of all routed slots and shared experts:
  *   y [N*k + S*N][H] (activation dtype) — rows [0, N*k) in expert-sorted order (the
  *   routing's perm), rows N*k + s*N + t for shared expert s and token t.
- * Requires a routing computed with the same workspace.
+ * Reads the routing's offsets and perm only (any workspace of the size
+ * yvmoe_workspace_bytes() gives will do: nothing from an earlier call is read from it).
  */
 int32_t yvmoe_expert_ffn(const void* x, int32_t act_dtype, int32_t n_tokens, int32_t top_k,
                          const yvmoe_expert_weights* experts, const yvmoe_routing* routing,
                          void* y, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * PiscesLxFusedMoEDispatch.forward (opss/infer/fused_moe.py:54-123) from a routing the caller
+ * computed with any router: routing_weights [N][k] (fp32 or bf16, weight_dtype = YVMOE_ACT_F32
+ * or YVMOE_ACT_BF16) and expert_indices [N][k] int64, k = slots_per_token (the indices' last
+ * dimension, fused_moe.py:76-82). On the device: counts = bincount(indices), offsets = their
+ * exclusive prefix sum, the stable expert-sorted order (argsort(stable=True), fused_moe.py:87),
+ * the grouped SwiGLU FFN of every slot (zero-weight slots included; the routed experts only —
+ * experts->num_shared is ignored), then
+ *   out[t] = round( sum_j w[t,j] * Y[t,j] )   (fp32, slot order j = 0..k-1, rounded once).
+ * A slot whose index lies outside [0, E) is not computed and adds nothing: the kernels never
+ * read out of bounds, and *invalid (int32 device scalar, may be NULL) receives the number of
+ * such slots so the caller can raise the reference's error. counts [E] / offsets [E+1] (int32,
+ * may be NULL) receive the reference's expert_counts / expert_offsets; y_out [N*k][H] (may be
+ * NULL) receives the expert outputs in expert-sorted order (for collect_stats). Nothing here
+ * synchronizes with the host. workspace: yvmoe_dispatch_workspace_bytes().
+ */
+size_t yvmoe_dispatch_workspace_bytes(int32_t n_tokens, int32_t act_dtype, int32_t slots_per_token,
+                                      const yvmoe_expert_weights* experts);
+int32_t yvmoe_dispatch(const void* x, int32_t act_dtype, int32_t n_tokens,
+                       const void* routing_weights, int32_t weight_dtype,
+                       const int64_t* expert_indices, int32_t slots_per_token,
+                       const yvmoe_expert_weights* experts, void* out, void* y_out,
+                       int32_t* counts, int32_t* offsets, int32_t* invalid, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /*
  * out[t] = sum_j weights[t,j] * y[pos[t*k+j]] + shared[t] + 0.1 * skip[t], accumulated in
@@ -305,9 +334,7 @@ int32_t yvmoe_moegate_logits(const void* x, int32_t act_dtype, int32_t n_tokens,
  * module state): yvmoe_moegate_logits, then the top-k routing of the logits (softmax, top_k,
  * softmax of the k scores, gate.py:393, :414-416) into `routing` (fixed mode: capacity -1),
  * with the expert counts, offsets and permutation of yvmoe_route.
- * workspace: at least yvmoe_moegate_forward_workspace_bytes(); the routing region sits at its
- * start, where yvmoe_expert_ffn expects it, so the same workspace can be handed to
- * yvmoe_expert_ffn next.
+ * workspace: at least yvmoe_moegate_forward_workspace_bytes().
  */
 size_t yvmoe_moegate_forward_workspace_bytes(int32_t n_tokens, int32_t act_dtype, int32_t top_k,
                                              const yvmoe_moegate* gate);

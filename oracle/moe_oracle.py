@@ -217,6 +217,66 @@ def swiglu(xs: torch.Tensor, wg: torch.Tensor, wu: torch.Tensor, wd: torch.Tenso
     return lin(F.silu(lin(xs, wg)) * lin(xs, wu), wd)
 
 
+@dataclass
+class OracleDispatch:
+    out: torch.Tensor        # [N, H] in x's dtype
+    counts: np.ndarray       # [E]
+    offsets: np.ndarray      # [E+1]
+    perm: np.ndarray         # [V] flat slots of the valid slots in expert-sorted order
+    Y: torch.Tensor          # [V, H] fp32 expert outputs (values of x's dtype) in that order
+    invalid: int             # slots whose index lies outside [0, E)
+
+
+def dispatch_forward(x2d: torch.Tensor, weights, indices, num_experts: int, expert_fn,
+                     tokens: Optional[np.ndarray] = None, lin=None) -> OracleDispatch:
+    """``PiscesLxFusedMoEDispatch.forward`` (opss/infer/fused_moe.py:54-123) given the
+    routing: ``token_ids = arange(N).repeat_interleave(k)`` (:83-84), a stable argsort of the
+    flat indices (:87), ``bincount`` / ``cumsum`` offsets (:93-95), the gathered rows of each
+    active expert through ``YvSwiGLUExpert.forward`` (:103-111) — ``expert_fn(e)`` returns its
+    (Wg, Wu, Wd) as fp32 — and the weighted combine (:117-119), summed per token in fp32 in
+    slot order and rounded once to x's dtype (the build's statement of the index_add_, whose
+    dtype and order the reference leaves to torch). Slots with an index outside [0, E) are
+    counted in ``invalid`` and add nothing (the reference raises on them). ``tokens``
+    restricts the expert math to a subset of tokens (other rows stay zero)."""
+    lin = linear if lin is None else lin
+    dtype = x2d.dtype
+    N, H = x2d.shape
+    idx = np.asarray(indices, dtype=np.int64).reshape(N, -1)
+    k = idx.shape[1]
+    w = torch.as_tensor(np.asarray(weights, dtype=np.float32)).reshape(N, k)
+    flat = idx.reshape(-1)
+    ok = (flat >= 0) & (flat < num_experts)
+    valid_slots = np.nonzero(ok)[0]
+    order = np.argsort(flat[valid_slots], kind="stable")
+    perm = valid_slots[order].astype(np.int64)
+    counts = np.bincount(flat[valid_slots], minlength=num_experts).astype(np.int64)
+    offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.int64)
+    keep = np.ones(N, dtype=bool)
+    if tokens is not None:
+        keep[:] = False
+        keep[np.asarray(tokens)] = True
+    token_of = perm // k
+    Y = torch.zeros(len(perm), H, dtype=torch.float32)
+    for e in range(num_experts):
+        a, b = int(offsets[e]), int(offsets[e + 1])
+        sel = np.arange(a, b)[keep[token_of[a:b]]]
+        if len(sel) == 0:
+            continue
+        rows = torch.from_numpy(token_of[sel])
+        wg, wu, wd = expert_fn(e)
+        Y[torch.from_numpy(sel)] = swiglu(x2d[rows], wg.to(dtype), wu.to(dtype), wd.to(dtype), lin).float()
+    pos = np.full(N * k, -1, dtype=np.int64)
+    pos[perm] = np.arange(len(perm))
+    acc = torch.zeros(N, H, dtype=torch.float32)
+    pos_t = torch.from_numpy(pos.reshape(N, k))
+    for j in range(k):
+        live = pos_t[:, j] >= 0
+        rows = torch.nonzero(live).reshape(-1)
+        if len(rows):
+            acc[rows] = acc[rows] + w[rows, j:j + 1] * Y[pos_t[rows, j]]
+    return OracleDispatch(acc.to(dtype), counts, offsets, perm, Y, int((~ok).sum()))
+
+
 def layer_forward(x2d: torch.Tensor, params: LayerParams, logits: Optional[np.ndarray] = None,
                   cap: Optional[int] = None, skip: Optional[torch.Tensor] = None,
                   routing: Optional[OracleRouting] = None,

@@ -45,6 +45,8 @@ EXPORTED_SYMBOLS = (
     "yvmoe_router_logits",
     "yvmoe_route",
     "yvmoe_expert_ffn",
+    "yvmoe_dispatch_workspace_bytes",
+    "yvmoe_dispatch",
     "yvmoe_combine",
     "yvmoe_forward",
     "yvmoe_forward_static",
@@ -171,6 +173,11 @@ def _declare(l: ctypes.CDLL) -> None:
     l.yvmoe_expert_ffn.restype = i32
     l.yvmoe_expert_ffn.argtypes = [vp, i32, i32, i32, ctypes.POINTER(ExpertWeights),
                                    ctypes.POINTER(Routing), vp, vp, sz, vp]
+    l.yvmoe_dispatch_workspace_bytes.restype = sz
+    l.yvmoe_dispatch_workspace_bytes.argtypes = [i32, i32, i32, ctypes.POINTER(ExpertWeights)]
+    l.yvmoe_dispatch.restype = i32
+    l.yvmoe_dispatch.argtypes = [vp, i32, i32, vp, i32, vp, i32, ctypes.POINTER(ExpertWeights),
+                                 vp, vp, vp, vp, vp, vp, sz, vp]
     l.yvmoe_combine.restype = i32
     l.yvmoe_combine.argtypes = [vp, i32, i32, i32, i32, i32, ctypes.POINTER(Routing), vp, vp,
                                 vp, vp, vp]

@@ -180,6 +180,65 @@ int32_t yvmoe_expert_ffn(const void* x, int32_t act_dtype, int32_t n_tokens, int
                              (hipStream_t)stream);
 }
 
+size_t yvmoe_dispatch_workspace_bytes(int32_t n_tokens, int32_t act_dtype, int32_t slots_per_token,
+                                      const yvmoe_expert_weights* experts) {
+    if (n_tokens < 0 || experts == nullptr || slots_per_token < 1 || slots_per_token > YVMOE_MAX_TOPK)
+        return 0;
+    return dispatch_ws(n_tokens, slots_per_token, experts->num_routed, experts->hidden, experts->ffn,
+                       act_dtype).bytes;
+}
+
+int32_t yvmoe_dispatch(const void* x, int32_t act_dtype, int32_t n_tokens,
+                       const void* routing_weights, int32_t weight_dtype,
+                       const int64_t* expert_indices, int32_t slots_per_token,
+                       const yvmoe_expert_weights* experts, void* out, void* y_out,
+                       int32_t* counts, int32_t* offsets, int32_t* invalid, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+    clear_error();
+    int rc = check_experts(experts, act_dtype);
+    if (rc) return rc;
+    const int N = n_tokens, k = slots_per_token, E = experts->num_routed;
+    YV_REQUIRE(N >= 0, YVMOE_ERR_ARG, "n_tokens=%d < 0", N);
+    YV_REQUIRE(k >= 1 && k <= YVMOE_MAX_TOPK, YVMOE_ERR_SHAPE, "slots_per_token=%d outside [1, %d]",
+               k, YVMOE_MAX_TOPK);
+    YV_REQUIRE(weight_dtype == YVMOE_ACT_F32 || weight_dtype == YVMOE_ACT_BF16, YVMOE_ERR_DTYPE,
+               "routing weights must be fp32 or bf16 (got dtype %d)", weight_dtype);
+    YV_REQUIRE((long long)N * k < (1ll << 31) && (long long)N * k * experts->hidden < (1ll << 40),
+               YVMOE_ERR_SHAPE, "problem too large");
+    const DispatchWs L = dispatch_ws(N, k, E, experts->hidden, experts->ffn, act_dtype);
+    YV_REQUIRE(workspace != nullptr && workspace_bytes >= L.bytes, YVMOE_ERR_WORKSPACE,
+               "workspace %zu bytes, need %zu", workspace_bytes, L.bytes);
+    YV_REQUIRE(N == 0 || (x && out && routing_weights && expert_indices), YVMOE_ERR_ARG,
+               "NULL pointer");
+    YV_REQUIRE(((uintptr_t)x | (uintptr_t)out | (uintptr_t)y_out | (uintptr_t)workspace) % 16 == 0,
+               YVMOE_ERR_ARG, "x, out, y_out and workspace must be 16-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    char* ws = (char*)workspace;
+    int* cnt = counts != nullptr ? counts : (int*)(ws + L.counts);
+    int* off = offsets != nullptr ? offsets : (int*)(ws + L.offsets);
+    int* misc = (int*)(ws + L.misc);
+    int* inv = invalid != nullptr ? invalid : misc + 1;
+    int* perm = (int*)(ws + L.perm);
+    int* pos = (int*)(ws + L.pos);
+    const bool wbf = weight_dtype == YVMOE_ACT_BF16;
+    float* w32 = wbf ? (float*)(ws + L.w32) : nullptr;
+    rc = dispatch_route_launch(expert_indices, wbf ? (const unsigned short*)routing_weights : nullptr,
+                               w32, N, E, k, cnt, off, perm, pos, inv, misc, ws, st);
+    if (rc || N == 0) return rc;
+    yvmoe_expert_weights routed = *experts;
+    routed.num_shared = 0;  // the dispatch runs the routed experts only (fused_moe.py:103-111)
+    yvmoe_routing r{};
+    r.weights = wbf ? w32 : (float*)routing_weights;
+    r.counts = cnt;
+    r.offsets = off;
+    r.perm = perm;
+    r.pos = pos;
+    void* y = y_out != nullptr ? y_out : (void*)(ws + L.y);
+    rc = expert_ffn_launch(x, act_dtype, N, k, &routed, &r, y, ws, st);
+    if (rc) return rc;
+    return combine_launch(y, act_dtype, N, experts->hidden, k, 0, &r, nullptr, nullptr, out, nullptr, st);
+}
+
 int32_t yvmoe_combine(const void* y, int32_t act_dtype, int32_t n_tokens, int32_t hidden,
                       int32_t top_k, int32_t num_shared, const yvmoe_routing* routing,
                       const float* mix, const void* skip, void* out, void* shared_out,

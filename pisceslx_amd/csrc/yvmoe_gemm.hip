@@ -65,7 +65,8 @@ enum Epi { EPI_F32 = 0, EPI_SWIGLU = 1, EPI_DOWN = 2 };
 struct GemmParams {
     const void* A;
     int lda;
-    const int* rowmap;  // sorted row -> token for routed rows; nullptr: A row = row
+    const int* rowmap;  // sorted row -> flat slot (the routing's perm); nullptr: A row = row
+    int rowdiv;         // slots per token: token of a routed row = rowmap[row] / rowdiv
     int routed_rows;    // rows >= routed_rows are shared rows (token = (row - routed) % ntok)
     int ntok;
     const void* B0;
@@ -246,7 +247,7 @@ struct BLoad<YVMOE_W_FP8> {
 
 __device__ __forceinline__ int map_row(const GemmParams& p, int row) {
     if (p.rowmap == nullptr) return row;
-    if (row < p.routed_rows) return p.rowmap[row];
+    if (row < p.routed_rows) return p.rowmap[row] / p.rowdiv;
     return (row - p.routed_rows) % p.ntok;
 }
 
@@ -1261,20 +1262,26 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
         }
     };
     float tmp[VEC];
+    // a slot without a position (pos < 0: an expert id outside [0, E) handed to the dispatch
+    // entry) has no expert output and adds nothing
     for (int j0 = 0; j0 < k; j0 += KC) {
         float wj[KC];
         Raw q[KC];
+        bool live[KC];
 #pragma unroll
         for (int i = 0; i < KC; ++i) {
+            live[i] = false;
             if (j0 + i < k) {
                 const long long sl = (long long)t * k + j0 + i;
+                const int pr = pos[sl];
+                live[i] = pr >= 0;
                 wj[i] = w[sl];
-                q[i] = raw_load(pos[sl]);
+                if (live[i]) q[i] = raw_load(pr);
             }
         }
 #pragma unroll
         for (int i = 0; i < KC; ++i) {
-            if (j0 + i < k) {
+            if (live[i]) {
                 unpack(q[i], tmp);
 #pragma unroll
                 for (int v = 0; v < VEC; ++v) acc[v] = acc[v] + wj[i] * tmp[v];
@@ -1639,7 +1646,8 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     // GEMM1: h = silu(x Wg^T) * (x Wu^T) over gathered rows
     p.A = x;
     p.lda = H;
-    p.rowmap = (const int*)(ws + RL.tok);
+    p.rowmap = routing->perm;
+    p.rowdiv = k;
     p.routed_rows = N * k;
     p.ntok = N;
     p.B0 = w->w_gate;

@@ -107,10 +107,11 @@ inline int max_tiles(int N, int k, int E, int S, int tile_rows) {
     return ceil_div(N * k, tile_rows) + E + S * ceil_div(N, tile_rows);
 }
 
-// Workspace layout. The routing region depends on (N, E, k) only, so yvmoe_route and
-// yvmoe_expert_ffn agree on it without knowing each other's arguments.
+// Workspace layout. The routing region depends on (N, E, k) only; the FFN region follows
+// it, so every entry that runs the expert FFN finds its region at the same offset. The FFN
+// reads nothing of the routing region: its inputs are the routing's offsets and perm.
 struct RouteWs {
-    size_t topp, w0, allowed, blockhist, blockoff, blocksum, tok, score, bytes;
+    size_t topp, w0, allowed, blockhist, blockoff, blocksum, score, bytes;
 };
 struct FfnWs {
     size_t seg, tile_seg, tile_row0, ntiles, h, bytes;
@@ -127,7 +128,6 @@ inline RouteWs route_ws(int N, int E, int k) {
     w.blockhist = o; o = align_up(o + (size_t)nb * E * 4, 256);
     w.blockoff = o;  o = align_up(o + (size_t)nb * E * 4, 256);
     w.blocksum = o;  o = align_up(o + (size_t)nb * 4, 256);
-    w.tok = o;       o = align_up(o + nk * 4 + 4, 256);
     w.score = o;     o = align_up(o + (size_t)N * 4, 256);
     w.bytes = o;
     return w;
@@ -152,6 +152,28 @@ inline FfnWs ffn_ws(int N, int k, int E, int S, int F, int act) {
 inline size_t y_bytes(int N, int k, int S, int H, int act) {
     const size_t R = (size_t)N * k + (size_t)S * N;
     return align_up(R * (size_t)H * (act == YVMOE_ACT_BF16 ? 2 : 4), 256);
+}
+
+// Workspace of yvmoe_dispatch (k = slots per token, routed experts only): the routing region
+// (block histograms and offsets), the FFN region after it (where expert_ffn_launch looks for
+// it), the expert outputs, then fp32 routing weights, the permutation and its inverse, counts,
+// offsets and two scalars (capacity, invalid-slot count).
+struct DispatchWs {
+    size_t y, w32, perm, pos, counts, offsets, misc, bytes;
+};
+inline DispatchWs dispatch_ws(int N, int k, int E, int H, int F, int act) {
+    DispatchWs w{};
+    const size_t nk = (size_t)N * k;
+    size_t o = route_ws(N, E, k).bytes + ffn_ws(N, k, E, 0, F, act).bytes;
+    w.y = o;       o += y_bytes(N, k, 0, H, act);
+    w.w32 = o;     o = align_up(o + nk * 4, 256);
+    w.perm = o;    o = align_up(o + nk * 4, 256);
+    w.pos = o;     o = align_up(o + nk * 4, 256);
+    w.counts = o;  o = align_up(o + (size_t)E * 4, 256);
+    w.offsets = o; o = align_up(o + (size_t)(E + 1) * 4, 256);
+    w.misc = o;    o = align_up(o + 2 * 4, 256);
+    w.bytes = o;
+    return w;
 }
 
 // ---------------------------------------------------------------- launchers
@@ -195,6 +217,12 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
                  const yvmoe_router* r, int cap_override, yvmoe_routing* out, char* ws,
                  hipStream_t st, int ksplit = 1, long long split_stride = 0,
                  const TileTable* tiles = nullptr);
+// external routing of the dispatch entry (yvmoe_route.hip): counts, offsets, the stable
+// permutation and its inverse (pos = -1 for ids outside [0, E)), the invalid-slot count, and
+// with w32 set the bf16 weights widened to fp32.
+int dispatch_route_launch(const int64_t* idx, const unsigned short* w_bf16, float* w32, int N,
+                          int E, int k, int* counts, int* offsets, int* perm, int* pos,
+                          int* invalid, int* cap_scratch, char* ws, hipStream_t st);
 // GEMMs and combine (yvmoe_gemm.hip). With reduce = false the router GEMM leaves its split-K
 // partial sums in partials (when it splits) for the routing kernel to reduce.
 int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, float* out,

@@ -216,14 +216,19 @@ __global__ __launch_bounds__(1024) void route_topk_kernel(
 }
 
 // cap_mode: 0 = no capacity (fixed_shape_mode), 1 = explicit, 2 = dynamic, 3 = static factor
+// blockinv / invalid_out (the dispatch entry; NULL otherwise): per-block counts of slots
+// with an expert id outside [0, E), summed into *invalid_out.
 __global__ __launch_bounds__(1024) void route_scan_kernel(
     const int* __restrict__ blockhist, int nb, int E, int N, const float* __restrict__ blocksum,
     int cap_mode, int cap_explicit, int min_cap, double cap_factor, int* __restrict__ counts,
-    int* __restrict__ offsets, int* __restrict__ blockoff, int* __restrict__ cap_out) {
+    int* __restrict__ offsets, int* __restrict__ blockoff, int* __restrict__ cap_out,
+    const int* __restrict__ blockinv = nullptr, int* __restrict__ invalid_out = nullptr) {
     __shared__ int part[1024];
     __shared__ int scan[YVMOE_MAX_EXPERTS];
     __shared__ float red[1024];
+    __shared__ int s_inv;
     const int tid = threadIdx.x;
+    if (tid == 0) s_inv = 0;
     const int C = 1024 / E;  // chunks of blocks per expert (E <= 256 -> C >= 4)
     const int e = tid % E;
     const int c = tid / E;
@@ -264,9 +269,16 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(
         if (tid < E) scan[tid] += v;
         __syncthreads();
     }
+    if (invalid_out != nullptr) {
+        int inv = 0;
+        for (int b = tid; b < nb; b += 1024) inv += blockinv[b];
+        if (inv) atomicAdd(&s_inv, inv);
+    }
+    __syncthreads();
     if (tid < E) offsets[tid + 1] = scan[tid];
     if (tid == 0) {
         offsets[0] = 0;
+        if (invalid_out != nullptr) *invalid_out = s_inv;
         int cap = -1;
         if (cap_mode == 1) {
             cap = cap_explicit;
@@ -298,10 +310,13 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(
 }
 
 // Stable scatter into expert-sorted order: the rank of a slot among same-expert slots of
-// its 64-slot chunk comes from 8 wavefront ballots over the expert id bits.
+// its 64-slot chunk comes from 8 wavefront ballots over the expert id bits. A slot whose
+// expert id lies outside [0, E) (external indices of the dispatch entry) takes no position:
+// pos = -1, and it is left out of every rank and count.
+template <typename IdxT>
 __global__ __launch_bounds__(256) void route_scatter_kernel(
-    const int64_t* __restrict__ idx, int N, int E, int k, const int* __restrict__ blockoff,
-    int* __restrict__ perm, int* __restrict__ pos, int* __restrict__ tok) {
+    const IdxT* __restrict__ idx, int N, int E, int k, const int* __restrict__ blockoff,
+    int* __restrict__ perm, int* __restrict__ pos) {
     __shared__ int cnt[YVMOE_MAX_TOPK][YVMOE_MAX_EXPERTS];
     __shared__ unsigned short rk[kTokPerBlock * YVMOE_MAX_TOPK];
     const int tid = threadIdx.x;
@@ -312,12 +327,22 @@ __global__ __launch_bounds__(256) void route_scatter_kernel(
     const int nslots = (int)((total - base) < (long long)kTokPerBlock * k ? (total - base)
                                                                           : (long long)kTokPerBlock * k);
     const int nchunks = (nslots + 63) / 64;
+    auto expert_of = [&](int s, bool& ok) {
+        const long long v = (long long)idx[base + s];
+        ok = v >= 0 && v < E;
+        return ok ? (int)v : 0;
+    };
     for (int q = tid; q < nchunks * E; q += 256) cnt[q / E][q % E] = 0;
     __syncthreads();
     for (int c = wave; c < nchunks; c += 4) {
         const int s = c * 64 + lane;
-        const bool valid = s < nslots;
-        const int e = valid ? (int)idx[base + s] : 0;
+        bool valid = s < nslots;
+        int e = 0;
+        if (valid) {
+            bool ok;
+            e = expert_of(s, ok);
+            valid = ok;
+        }
         unsigned long long mask = __ballot(valid);
 #pragma unroll
         for (int bit = 0; bit < 8; ++bit) {
@@ -342,12 +367,16 @@ __global__ __launch_bounds__(256) void route_scatter_kernel(
     }
     __syncthreads();
     for (int s = tid; s < nslots; s += 256) {
-        const int e = (int)idx[base + s];
-        const int p = blockoff[(size_t)blockIdx.x * E + e] + cnt[s / 64][e] + rk[s];
+        bool ok;
+        const int e = expert_of(s, ok);
         const long long slot = base + s;
+        if (!ok) {
+            pos[slot] = -1;
+            continue;
+        }
+        const int p = blockoff[(size_t)blockIdx.x * E + e] + cnt[s / 64][e] + rk[s];
         perm[p] = (int)slot;
         pos[slot] = p;
-        tok[p] = (int)(slot / k);
     }
 }
 
@@ -539,7 +568,6 @@ struct SmallRouteArgs {
     int* perm;
     int* pos;
     int* cap_out;
-    int* tok;
     TileTable tiles;  // tiles.seg == nullptr: no tile table
 };
 
@@ -674,7 +702,6 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
         const int p = s_off[e] + cnt[s / 64][e] + s_rk[s];
         a.perm[p] = s;
         a.pos[s] = p;
-        a.tok[p] = s / k;
         s_perm[p] = (unsigned short)s;
     }
     __syncthreads();
@@ -760,7 +787,63 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ external routing
+// The dispatch entry (PiscesLxFusedMoEDispatch.forward, opss/infer/fused_moe.py:69-100) takes
+// the routing from its caller. One block per 64 tokens: the block's histogram of expert ids
+// in [0, E) and its count of ids outside that range (those slots are left out of the
+// permutation and the combine; the entry reports how many there were), and with w32 set the
+// bf16 routing weights widened to fp32 (exact).
+__global__ __launch_bounds__(256) void dispatch_hist_kernel(
+    const int64_t* __restrict__ idx, const unsigned short* __restrict__ w_bf16, int N, int E, int k,
+    float* __restrict__ w32, int* __restrict__ blockhist, int* __restrict__ blockinv) {
+    __shared__ int hist[YVMOE_MAX_EXPERTS];
+    __shared__ int s_inv;
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += 256) hist[e] = 0;
+    if (tid == 0) s_inv = 0;
+    __syncthreads();
+    const long long base = (long long)blockIdx.x * kTokPerBlock * k;
+    const long long total = (long long)N * k;
+    const long long span = total - base < (long long)kTokPerBlock * k ? total - base
+                                                                      : (long long)kTokPerBlock * k;
+    const int nslots = (int)span;
+    int inv = 0;
+    for (int s = tid; s < nslots; s += 256) {
+        const long long q = base + s;
+        const long long v = idx[q];
+        if (v >= 0 && v < E) atomicAdd(&hist[(int)v], 1);
+        else ++inv;
+        if (w32 != nullptr) w32[q] = __uint_as_float((unsigned)w_bf16[q] << 16);
+    }
+    if (inv) atomicAdd(&s_inv, inv);
+    __syncthreads();
+    for (int e = tid; e < E; e += 256) blockhist[(size_t)blockIdx.x * E + e] = hist[e];
+    if (tid == 0) blockinv[blockIdx.x] = s_inv;
+}
+
 }  // namespace
+
+int dispatch_route_launch(const int64_t* idx, const unsigned short* w_bf16, float* w32, int N,
+                          int E, int k, int* counts, int* offsets, int* perm, int* pos,
+                          int* invalid, int* cap_scratch, char* ws, hipStream_t st) {
+    const RouteWs L = route_ws(N, E, k);
+    int* blockhist = (int*)(ws + L.blockhist);
+    int* blockoff = (int*)(ws + L.blockoff);
+    int* blockinv = (int*)(ws + L.blocksum);  // the complexity sums' region: [nb] 4-byte slots
+    const int nb = ceil_div(N, kTokPerBlock);
+    if (N > 0) {
+        dispatch_hist_kernel<<<nb, 256, 0, st>>>(idx, w_bf16, N, E, k, w32, blockhist, blockinv);
+        YV_LAUNCH_CHECK("dispatch_hist");
+    }
+    route_scan_kernel<<<1, 1024, 0, st>>>(blockhist, nb, E, N, nullptr, 0, -1, 0, 1.0, counts,
+                                            offsets, blockoff, cap_scratch, blockinv, invalid);
+    YV_LAUNCH_CHECK("dispatch_scan");
+    if (N > 0) {
+        route_scatter_kernel<int64_t><<<nb, 256, 0, st>>>(idx, N, E, k, blockoff, perm, pos);
+        YV_LAUNCH_CHECK("dispatch_scatter");
+    }
+    return YVMOE_OK;
+}
 
 int route_launch(const float* logits, int ld, const float* pred, int pred_ld, int N,
                  const yvmoe_router* r, int cap_override, yvmoe_routing* out, char* ws,
@@ -773,7 +856,6 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
     int* blockhist = (int*)(ws + L.blockhist);
     int* blockoff = (int*)(ws + L.blockoff);
     float* blocksum = (float*)(ws + L.blocksum);
-    int* tok = (int*)(ws + L.tok);
     const int nb = ceil_div(N, kTokPerBlock);
     const bool fixed = r->fixed_shape_mode != 0;
     int cap_mode = 0;
@@ -813,7 +895,6 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
         a.perm = out->perm;
         a.pos = out->pos;
         a.cap_out = out->capacity;
-        a.tok = tok;
         if (tiles) a.tiles = *tiles;
         route_small_kernel<<<1, 1024, 0, st>>>(a);
         YV_LAUNCH_CHECK("route_small");
@@ -846,8 +927,8 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
                                             r->min_capacity, r->capacity_factor, out->counts,
                                             out->offsets, blockoff, out->capacity);
     YV_LAUNCH_CHECK("route_scan");
-    route_scatter_kernel<<<nb, 256, 0, st>>>(out->indices, N, E, k, blockoff, out->perm,
-                                             out->pos, tok);
+    route_scatter_kernel<int64_t><<<nb, 256, 0, st>>>(out->indices, N, E, k, blockoff, out->perm,
+                                                      out->pos);
     YV_LAUNCH_CHECK("route_scatter");
     if (!fixed) {
         capacity_trim_kernel<<<E, 256, 0, st>>>(out->counts, out->offsets, out->capacity,

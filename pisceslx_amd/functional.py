@@ -152,7 +152,10 @@ def route(logits: torch.Tensor, router: RouterState, predictor: bool = True,
 
 def expert_ffn(x2d: torch.Tensor, experts: PackedExperts, routing: Routing, top_k: int,
                workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """y [N*k + S*N, H]: expert outputs in expert-sorted order, then the shared experts."""
+    """y [N*k + S*N, H]: expert outputs in expert-sorted order, then the shared experts.
+
+    Reads the routing's offsets and permutation only; ``workspace`` is scratch (allocated
+    here when None or too small)."""
     dev = _require_cuda(x2d, *experts.tensors())
     act = _act(x2d.dtype)
     N = x2d.shape[0]
@@ -160,12 +163,64 @@ def expert_ffn(x2d: torch.Tensor, experts: PackedExperts, routing: Routing, top_
     y = torch.empty(R, experts.hidden, dtype=x2d.dtype, device=dev)
     e = experts.struct()
     o = routing.struct()
-    if workspace is None:
-        raise ValueError("expert_ffn needs the workspace the routing was computed in")
+    r = _lib.Router(experts.num_routed, experts.hidden, top_k, 0, 0, 0, 1.0, None, None, None,
+                    None, None)
+    need = int(_lib.lib().yvmoe_workspace_bytes(N, act, ctypes.byref(r), ctypes.byref(e)))
+    if workspace is None or workspace.numel() < need:
+        workspace = _workspace(need, dev)
     _lib.check(_lib.lib().yvmoe_expert_ffn(x2d.data_ptr(), act, N, top_k, ctypes.byref(e),
                                             ctypes.byref(o), y.data_ptr(), workspace.data_ptr(),
                                             workspace.numel(), _stream(dev)), "yvmoe_expert_ffn")
     return y
+
+
+def dispatch_workspace_bytes(n_tokens: int, act: int, slots: int, experts: PackedExperts) -> int:
+    e = experts.struct()
+    return int(_lib.lib().yvmoe_dispatch_workspace_bytes(n_tokens, act, slots, ctypes.byref(e)))
+
+
+def dispatch(x2d: torch.Tensor, routing_weights: torch.Tensor, expert_indices: torch.Tensor,
+             experts: PackedExperts, want_expert_outputs: bool = False,
+             workspace: Optional[torch.Tensor] = None):
+    """Dispatch of an external routing (yvmoe_dispatch): grouped SwiGLU of the routed experts
+    over every (token, slot) of ``expert_indices`` [N, k] int64 with ``routing_weights``
+    [N, k] (fp32 or bf16), combined per token. Nothing synchronizes with the host.
+
+    Returns (out [N, H], counts [E] int32, offsets [E+1] int32, invalid [1] int32 = number of
+    slots whose index lies outside [0, E), expert outputs [N*k, H] in expert-sorted order or
+    None).
+    """
+    dev = _require_cuda(x2d, routing_weights, expert_indices, *experts.tensors())
+    act = _act(x2d.dtype)
+    N, H = x2d.shape
+    if H != experts.hidden:
+        raise ValueError(f"hidden size {H} does not match the experts ({experts.hidden})")
+    if expert_indices.dtype != torch.int64 or expert_indices.dim() != 2 or expert_indices.shape[0] != N:
+        raise ValueError("expert_indices must be int64 [N, k]")
+    k = expert_indices.shape[1]
+    if tuple(routing_weights.shape) != (N, k):
+        raise ValueError(f"routing_weights must be [N, k] = [{N}, {k}]")
+    wdt = _act(routing_weights.dtype)
+    E = experts.num_routed
+    out = torch.empty_like(x2d)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    invalid = torch.empty(1, dtype=torch.int32, device=dev)
+    y = torch.empty(N * k, H, dtype=x2d.dtype, device=dev) if want_expert_outputs else None
+    need = dispatch_workspace_bytes(N, act, k, experts)
+    if need == 0:
+        raise ValueError(f"yvmoe_dispatch_workspace_bytes rejected k={k}")
+    if workspace is None or workspace.numel() < need:
+        workspace = _workspace(need, dev)
+    e = experts.struct()
+    _lib.check(_lib.lib().yvmoe_dispatch(
+        x2d.data_ptr() if N > 0 else None, act, N,
+        routing_weights.data_ptr() if N > 0 else None, wdt,
+        expert_indices.data_ptr() if N > 0 else None, k, ctypes.byref(e),
+        out.data_ptr() if N > 0 else None, _ptr(y) if N > 0 else None, counts.data_ptr(),
+        offsets.data_ptr(), invalid.data_ptr(), workspace.data_ptr(), workspace.numel(),
+        _stream(dev)), "yvmoe_dispatch")
+    return out, counts, offsets, invalid, y
 
 
 def moe_forward(x2d: torch.Tensor, router: RouterState, experts: PackedExperts,
@@ -320,8 +375,7 @@ def moegate_forward(x2d: torch.Tensor, gate: MoEGateState, top_k: int,
                     workspace: Optional[torch.Tensor] = None):
     """YvMoEGate logits [N, E], loss [1] and the fixed-mode routing, in one library call.
 
-    Returns (logits, loss, Routing, workspace); the workspace's routing region is what
-    expert_ffn reads, so it can be passed on to expert_ffn with the routing.
+    Returns (logits, loss, Routing, workspace); the routing can be passed on to expert_ffn.
     """
     dev = _require_cuda(x2d, modal_id, *gate.tensors())
     act = _act(x2d.dtype)
