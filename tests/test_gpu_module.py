@@ -129,6 +129,56 @@ def test_stable_gate_contract(cuda, oracle):
         gate.train()(x)
 
 
+@pytest.mark.parametrize("load_records", [4, 23])
+def test_stable_gate_load_adjustment_routing(cuda, oracle, load_records):
+    """A gate whose routing history is non-empty (gate.py:1192-1204): the adjustment
+    0.1 * (predicted - recent) is added to the logits before the softmax. Uniform prediction
+    below 10 load records, the LSTM's from 10 on. The GPU routing must equal the oracle's
+    routing of the GPU's fp32 logits with that bias, bit for bit, and differ from the routing
+    without it."""
+    E, H, k = 16, 256, 4
+    torch.manual_seed(3)
+    gate = YvStableMoEGate(H, E, top_k=k, min_capacity=2, device=cuda).eval()
+    rng = np.random.default_rng(load_records)
+    rows = rng.dirichlet(np.full(E, 0.8), size=6)          # skewed but above the 0.7 ratio
+    recent = rows.mean(0)
+    assert -(recent * np.log(recent)).sum() / np.log(E) > 0.75
+    with torch.no_grad():
+        gate.gate.weight.normal_(0.0, 0.02)
+        gate.routing_history[:6] = torch.tensor(rows, dtype=torch.float32)
+        gate.history_ptr.fill_(6)
+        gate.expert_load_buffer[:load_records] = torch.tensor(
+            rng.dirichlet(np.ones(E), size=load_records), dtype=torch.float32)
+        gate.load_buffer_ptr.fill_(load_records)
+        for p_ in gate.predictor_head.parameters():
+            p_.normal_(0.0, 2.0)                           # a prediction far from uniform
+    x = torch.randn(1, 96, H, device=cuda)
+    print(f"stable gate load adjustment, {load_records} load records", flush=True)
+    weights, indices, _ = gate(x)
+    adj = gate._load_adjustment()
+    assert adj is not None
+    st = gate.router_state(yvf._act(x.dtype))
+    assert st.bias is adj
+    lg = yvf.router_logits(x.reshape(-1, H).contiguous(), st)
+    torch.cuda.synchronize()
+    params = moe_oracle.LayerParams(
+        hidden=H, ffn=64, num_experts=E, num_shared=0, top_k=k,
+        gate_weight=gate.gate.weight.detach().cpu(),
+        pred=tuple(t.detach().cpu() for t in (gate.complexity_predictor[0].weight,
+                                              gate.complexity_predictor[0].bias,
+                                              gate.complexity_predictor[2].weight,
+                                              gate.complexity_predictor[2].bias)),
+        bias=None, fixed_shape_mode=False, dynamic_capacity=True, capacity_factor=1.0,
+        min_capacity=2, mix_param=None, expert_fn=None)
+    cap = moe_oracle.layer_capacity(params, x.reshape(-1, H).cpu())
+    lgn = lg[:, :E].cpu().numpy()
+    r = oracle.route(lgn, k, cap, adj.cpu().numpy())
+    assert np.array_equal(indices.cpu().numpy(), r.indices.astype(np.int64))
+    assert np.array_equal(weights.cpu().numpy().view(np.uint32), r.weights.view(np.uint32))
+    r0 = oracle.route(lgn, k, cap, None)
+    assert not np.array_equal(r0.indices, r.indices)       # the bias changed some choices
+
+
 def test_layer_rejects_training_mode(cuda):
     layer = YvDeepSeekMoELayer(Cfg(), device=cuda, dtype=torch.bfloat16, weight_format="bf16")
     with pytest.raises(NotImplementedError):
