@@ -35,6 +35,8 @@ Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
        python bench.py --pmc-probe {cfg2,cfg3}   (launches only, for counter runs)
 """
 import argparse
+import dataclasses
+import itertools
 import json
 import os
 import statistics
@@ -102,30 +104,60 @@ def measured_traffic():
         return None
 
 
-def time_layer(yvf, x, st, experts, mix, skip, ws, steps, warmup):
+def steady_state(fn, min_gpu_s=0.2, window=10, tol=0.02, max_windows=200):
+    """Warm-up by GPU time, not by call count: run windows of `window` calls (HIP events on
+    the current stream) until at least `min_gpu_s` of GPU work has run and two consecutive
+    windows agree within `tol`. A fresh GPU needs its clocks and power state to settle, which
+    a few calls do not give. Returns the last window's mean per call (seconds)."""
     import torch
+    stream = torch.cuda.current_stream()
+    total, prev, cur = 0.0, None, None
+    for _ in range(max_windows):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(window):
+            fn()
+        b.record(stream)
+        b.synchronize()
+        dt = a.elapsed_time(b) / 1e3
+        total += dt
+        cur = dt / window
+        if total >= min_gpu_s and prev is not None and abs(cur - prev) <= tol * prev:
+            break
+        prev = cur
+    return cur
+
+
+def time_layer(yvf, x, st, experts, mix, skip, ws, steps, warmup):
+    """Mean layer step: `warmup` calls, a warm-up to steady state by GPU time, then exactly
+    `steps` calls bracketed by device synchronizations (host clock)."""
+    import torch
+    fn = lambda: yvf.moe_forward(x, st, experts, mix, skip, workspace=ws)
     for _ in range(warmup):
-        yvf.moe_forward(x, st, experts, mix, skip, workspace=ws)
+        fn()
+    steady_state(fn)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(steps):
-        yvf.moe_forward(x, st, experts, mix, skip, workspace=ws)
+        fn()
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) / steps
 
 
 def time_ffn(yvf, x, st, experts, mix, skip, ws, k, steps):
-    """Average duration of the grouped expert FFN, HIP events on its stream."""
+    """Average duration of the grouped expert FFN, HIP events on its stream, after a warm-up
+    to steady state."""
     import torch
     out, shared, routing = yvf.moe_forward(x, st, experts, mix, skip, workspace=ws)
     stream = torch.cuda.current_stream()
-    for _ in range(3):
-        yvf.expert_ffn(x, experts, routing, k, workspace=ws)
+    fn = lambda: yvf.expert_ffn(x, experts, routing, k, workspace=ws)
+    steady_state(fn)
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     a.record(stream)
     for _ in range(steps):
-        yvf.expert_ffn(x, experts, routing, k, workspace=ws)
+        fn()
     b.record(stream)
     b.synchronize()
     return a.elapsed_time(b) / 1e3 / steps, routing
@@ -177,14 +209,20 @@ def moegate_bench(w, mix, steps, prefill_steps, lengths):
         gen = torch.Generator(device=dev).manual_seed(3)
         x = torch.randn(N, H, device=dev, generator=gen).to(torch.bfloat16)
         seq = 1 if name == "decode" else N  # decode: B x 1 tokens; prefill: one packed sequence
-        st = g.gate_state(_lib.ACT_BF16, seq)
-        P = st.w_proj.shape[0]
+        st0 = g.gate_state(_lib.ACT_BF16, seq)
+        P = st0.w_proj.shape[0]
+        # three copies of the 138 MB projection operand, used in turn, so the 256 MB Infinity
+        # Cache cannot serve the weights of one call from the call before
+        states = [st0] + [dataclasses.replace(st0, w_proj=st0.w_proj.clone()) for _ in range(2)]
         ws = torch.empty(max(256, int(_lib.lib().yvmoe_forward_moegate_workspace_bytes(
-            N, _lib.ACT_BF16, k, __import__("ctypes").byref(st.struct()),
+            N, _lib.ACT_BF16, k, __import__("ctypes").byref(st0.struct()),
             __import__("ctypes").byref(w.experts.struct())))), dtype=torch.uint8, device=dev)
-        t_gate = time_calls(lambda: yvf.moegate_forward(x, st, k, workspace=ws), n_steps, 3)
-        t_layer = time_calls(lambda: yvf.moe_forward_moegate(x, st, k, w.experts, mix, None,
-                                                              workspace=ws), n_steps, 3)
+        turn = itertools.cycle(range(3))
+        t_gate = time_calls(lambda: yvf.moegate_forward(x, states[next(turn)], k, workspace=ws),
+                            n_steps, 3)
+        t_layer = time_calls(lambda: yvf.moe_forward_moegate(x, states[next(turn)], k, w.experts,
+                                                              mix, None, workspace=ws), n_steps, 3)
+        del states
         wbytes = P * H * 2
         entry = {"tokens": N, "gate_ms_per_call": round(t_gate * 1e3, 4),
                  "gate_tokens_per_s": round(N / t_gate, 1),
@@ -227,28 +265,31 @@ def norm_bench(w, steps, lengths):
     res = {"workload": "two RMSNorms in sequence (YvHybridBlock norm_fusion, norm_mlp), hidden 4096, "
                        "bf16, one pass"}
     for name, N in (("decode", w.n_tokens), ("prefill", sum(lengths))):
-        x = torch.randn(N, H, device=dev, generator=gen).to(torch.bfloat16)
-        y = torch.empty_like(x)
-        reps = 50
+        # three input/output pairs used in turn: at prefill one pair is 274 MB, so the 256 MB
+        # Infinity Cache cannot hold the previous launch's rows
+        xs = [torch.randn(N, H, device=dev, generator=gen).to(torch.bfloat16) for _ in range(3)]
+        ys = [torch.empty_like(xs[0]) for _ in range(3)]
+        reps = 51
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream(dev))
         with torch.cuda.stream(side):
-            yvf.rms_norm(x, norms, out=y)          # warm the launch path outside the capture
+            yvf.rms_norm(xs[0], norms, out=ys[0])  # warm the launch path outside the capture
         torch.cuda.current_stream(dev).wait_stream(side)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            for _ in range(reps):
-                yvf.rms_norm(x, norms, out=y)
+            for i in range(reps):
+                yvf.rms_norm(xs[i % 3], norms, out=ys[i % 3])
         t = time_calls(graph.replay, max(3, steps // 10), 2) / reps
         nbytes = 2 * N * H * 2 + 2 * H * 2
         achieved = nbytes / t / 1e9
         res[name] = {"tokens": N, "us_per_call": round(t * 1e6, 3),
-                     "timing": "HIP graph of 50 launches, per node (includes the graph's per-node "
-                               "launch cost, which dominates a kernel of a few us)",
+                     "timing": "HIP graph of 51 launches over three buffer pairs in turn, per node "
+                               "(includes the graph's per-node launch cost, which dominates a "
+                               "kernel of a few us)",
                      "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                                   "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
                                   "kernel": "rmsnorm_kernel (2 norms)", "algorithmic_bytes": nbytes}}
-        del graph, x, y
+        del graph, xs, ys
     return res
 
 
@@ -285,28 +326,57 @@ def other_configs(names, steps):
     return res
 
 
-def cpu_baseline(w, budget_s=30.0):
-    """The CPU oracle (reference algorithm restated with torch on the host), bounded."""
-    import torch
-    from oracle import moe_oracle
-    cores = max(1, min(16, len(os.sched_getaffinity(0))))
-    torch.set_num_threads(cores)
-    params = moe_oracle.params_from_workload(w)
-    x = w.x.cpu()
+def cpu_model_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_time(fn, budget_s):
+    """1 warm-up, then the median of up to 3 timed runs within budget_s."""
     times = []
     t_start = time.perf_counter()
-    moe_oracle.layer_forward(x, params, reference_linear=True)  # warm-up
+    fn()
     for _ in range(3):
         if time.perf_counter() - t_start > budget_s and times:
             break
         t0 = time.perf_counter()
-        moe_oracle.layer_forward(x, params, reference_linear=True)
+        fn()
         times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    return {"value": round(w.n_tokens / t, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": f"{w.spec.name} full forward, {w.n_tokens} tokens, 1 warm-up + median of "
-                      f"{len(times)} runs ({t:.3f} s each), experts dequantized inside the loop, "
-                      f"bf16 F.linear as the reference runs it"}
+    return statistics.median(times), len(times)
+
+
+def cpu_baseline(w, x3=None, budget_s=30.0):
+    """The CPU oracle (the reference algorithm restated with torch on the host: router and
+    routing, per-expert loop with experts dequantized inside it, bf16 F.linear as the reference
+    runs it, shared experts, combine) on every core this process may use, bounded. The cfg2
+    decode batch is timed whole; for cfg3 (prefill) a leading slice of the packed batch is
+    timed (the per-token cost of the full 16K-token forward, which would take minutes)."""
+    import torch
+    from oracle import moe_oracle
+    cores = max(1, len(os.sched_getaffinity(0)))
+    torch.set_num_threads(cores)
+    params = moe_oracle.params_from_workload(w)
+    x = w.x.cpu()
+    t, n = _cpu_time(lambda: moe_oracle.layer_forward(x, params, reference_linear=True), budget_s)
+    res = {"value": round(w.n_tokens / t, 2), "unit": "tokens/s", "cores": cores, "kind": "port",
+           "cpu": cpu_model_name(),
+           "sample": f"{w.spec.name} full forward, {w.n_tokens} tokens, 1 warm-up + median of "
+                     f"{n} runs ({t:.3f} s each), experts dequantized inside the loop, "
+                     f"bf16 F.linear as the reference runs it, {cores} threads"}
+    if x3 is not None:
+        n_tok = x3.shape[0]
+        t3, n3 = _cpu_time(lambda: moe_oracle.layer_forward(x3, params, reference_linear=True),
+                           budget_s)
+        res["cfg3"] = {"value": round(n_tok / t3, 2), "unit": "tokens/s",
+                       "sample": f"cfg3 layer on the first {n_tok} tokens of the packed prefill "
+                                 f"batch, 1 warm-up + median of {n3} runs ({t3:.3f} s each)"}
+    return res
 
 
 def main():
@@ -364,6 +434,7 @@ def main():
     layer_bytes = work["weight_bytes"] + spec.num_experts * H * 2 + 64 * H * 4 + N * H * 2 * 4
     result["layer_hbm_gbs"] = round(layer_bytes / t_step / 1e9, 1)
 
+    x3_cpu = None
     if not args.no_prefill:
         lengths = seq_lengths("cfg3", 0)
         Np = sum(lengths)
@@ -385,6 +456,7 @@ def main():
                          "kernel": "grouped expert FFN (yvmoe_expert_ffn)",
                          "ms_per_launch": round(tpf * 1e3, 4), "algorithmic_flops": wp["flops"]},
         }
+        x3_cpu = xp[:1024].cpu()
         del xp, skip_p, wsp
     if not args.no_moegate:
         result["moegate"] = moegate_bench(w, mix, args.steps, args.prefill_steps, seq_lengths("cfg3", 0))
@@ -393,7 +465,7 @@ def main():
     if not args.no_other_configs:
         result["other_configs"] = other_configs(("cfg1", "cfg4", "cfg5"), max(5, args.prefill_steps // 2))
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(w)
+        result["cpu_baseline"] = cpu_baseline(w, x3_cpu)
     print(json.dumps(result), flush=True)
 
 

@@ -78,6 +78,7 @@ def _check_dispatch(oracle, w, idx, wts, label, tokens=None, weight_dtype=torch.
     ("cfg2", {"n_tokens": 700}, 6),
     ("cfg4", {"n_tokens": 96}, 8),
     ("cfg5", {"n_tokens": 200, "num_experts": 32}, 8),
+    ("cfg5", {"n_tokens": 64, "num_experts": 32}, 8),   # fp8 weights on the streaming form
 ])
 def test_dispatch_matches_oracle(cuda, oracle, name, kw, k):
     w = make_workload(name, device=cuda, **kw)

@@ -74,6 +74,7 @@ def _run_and_check(oracle, w, skip=None, tokens=None, label=None):
     ("cfg3", {"n_tokens": 512}),
     ("cfg4", {"n_tokens": 384}),
     ("cfg5", {"n_tokens": 384, "num_experts": 32}),
+    ("cfg5", {"n_tokens": 64, "num_experts": 32}),       # fp8 weights on the streaming form
 ])
 def test_layer_matches_oracle(cuda, oracle, name, kw):
     w = make_workload(name, device="cuda", **kw)
