@@ -36,6 +36,12 @@
 #ifndef YV_NB2
 #define YV_NB2 1  // column blocks per wavefront, streaming down projection (1 measured best)
 #endif
+#ifndef YV_U1
+#define YV_U1 4  // k-steps per staged chunk, streaming gate/up
+#endif
+#ifndef YV_U2
+#define YV_U2 4  // k-steps per staged chunk, streaming down projection
+#endif
 
 namespace yvmoe {
 namespace {
@@ -530,16 +536,11 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
 #pragma unroll
         for (int rb = 0; rb < MAXRB; ++rb) acc[b][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    {
-        uint4 v[PER_THREAD];
-        stage_load(0, v);
-        stage_store(0, v);
-    }
-    __syncthreads();
-    for (int c = 0; c < nchunks; ++c) {
+    // weights of chunk c (the tile's expert is all they depend on)
+    typename BL::Raw bw[NB][U];
+    float sg[NB][U];
+    auto load_w = [&](int c) {
         const int ks0 = c * U;
-        typename BL::Raw bw[NB][U];
-        float sg[NB][U];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             if (active[b]) {
@@ -552,6 +553,19 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
                 }
             }
         }
+    };
+    // chunk 0's weight loads go out before the activation staging, which waits on the row map
+    // and the activation loads: the first weights are in flight during that chain
+    load_w(0);
+    {
+        uint4 v[PER_THREAD];
+        stage_load(0, v);
+        stage_store(0, v);
+    }
+    __syncthreads();
+    for (int c = 0; c < nchunks; ++c) {
+        const int ks0 = c * U;
+        if (c > 0) load_w(c);
         uint4 nxt[PER_THREAD];
         if (c + 1 < nchunks) stage_load(c + 1, nxt);
         const uint4* arow = &As[c & 1][(lane & 15) * ROW_U4 + (lane >> 4) * 2];
@@ -1665,7 +1679,7 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.kchunk = H;
     const bool streaming = (maxrb == 1);
     int rc = tiled ? tile_dispatch<EPI_SWIGLU>(wf, p, T, st, "expert_gemm1", tt.fold > 0)
-           : streaming ? stream_dispatch<EPI_SWIGLU, 4, YV_NB1>(wf, p, T, st, "expert_gemm1")
+           : streaming ? stream_dispatch<EPI_SWIGLU, YV_U1, YV_NB1>(wf, p, T, st, "expert_gemm1")
                        : gemm_dispatch<EPI_SWIGLU>(act, wf, p, T, (F % 32 == 0) ? 2 : 1, 1, st,
                                                    "expert_gemm1", maxrb);
     if (rc != YVMOE_OK) return rc;
@@ -1687,7 +1701,7 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.ldo = H;
     p.kchunk = F;
     if (tiled) return tile_dispatch<EPI_DOWN>(wf, p, T, st, "expert_gemm2", tt.fold > 0);
-    return streaming ? stream_dispatch<EPI_DOWN, 4, YV_NB2>(wf, p, T, st, "expert_gemm2")
+    return streaming ? stream_dispatch<EPI_DOWN, YV_U2, YV_NB2>(wf, p, T, st, "expert_gemm2")
                      : gemm_dispatch<EPI_DOWN>(act, wf, p, T, (H % 32 == 0) ? 2 : 1, 1, st,
                                                "expert_gemm2", maxrb);
 }
