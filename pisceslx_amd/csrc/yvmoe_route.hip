@@ -520,9 +520,21 @@ __global__ __launch_bounds__(256) void route_topk_small_kernel(
     float* __restrict__ score) {
     __shared__ float s_lg[16 * NV];
     __shared__ float s_pr[kMaxPredTerms * kPredDim];
+    __shared__ float s_bias[16 * NV];
+    __shared__ float s_b1[kPredDim], s_w2[kPredDim], s_b2[1];
     const int tid = threadIdx.x;
     const int t = blockIdx.x;
     const int npc = (pred != nullptr) ? pred_terms * kPredDim : 0;
+    // the bias and predictor constants into LDS, loaded alongside the partial sums below
+    // (the top-k and predictor then wait on one round of global loads, not two)
+    if (bias != nullptr && tid < E) s_bias[tid] = bias[tid];
+    if (pred != nullptr) {
+        if (tid < kPredDim) {
+            s_b1[tid] = b1[tid];
+            s_w2[tid] = w2[tid];
+        }
+        if (tid == kPredDim) s_b2[0] = b2[0];
+    }
     for (int c = tid; c < E + npc; c += 256) {
         const float* base = (c < E) ? logits + (size_t)t * ld + c : pred + (size_t)t * ld + (c - E);
         // unconditional loads (split index clamped): no branch, so all are in flight together
@@ -541,7 +553,8 @@ __global__ __launch_bounds__(256) void route_topk_small_kernel(
     const int l = tid;
     int my_id;
     float my_ts, my_w0;
-    topk_token<NV>([&](int e) { return s_lg[e]; }, bias, l, E, k, my_id, my_ts, my_w0);
+    topk_token<NV>([&](int e) { return s_lg[e]; }, bias != nullptr ? s_bias : nullptr, l, E, k, my_id,
+                   my_ts, my_w0);
     if (l < k) {
         const size_t s = (size_t)t * k + l;
         idx_out[s] = (int64_t)my_id;
@@ -549,7 +562,7 @@ __global__ __launch_bounds__(256) void route_topk_small_kernel(
         w0[s] = my_w0;
     }
     if (pred != nullptr) {
-        const float sv = predictor_token([&](int c) { return s_pr[c]; }, pred_terms, b1, w2, b2, l);
+        const float sv = predictor_token([&](int c) { return s_pr[c]; }, pred_terms, s_b1, s_w2, s_b2, l);
         if (l == 0) score[t] = sv;
     }
 }
@@ -591,6 +604,7 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
     __shared__ unsigned short s_rk[kSmallSlots];
     __shared__ unsigned short s_perm[kSmallSlots];
     __shared__ float s_topp[kSmallSlots];
+    __shared__ float s_w0[kSmallSlots];
     __shared__ float s_score[kSmallRouteTok];
     __shared__ int s_cap;
     const int tid = threadIdx.x;
@@ -608,6 +622,7 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
         const int e = (int)a.indices[s];
         s_idx[s] = (unsigned char)e;
         s_topp[s] = a.topp[s];
+        s_w0[s] = a.w0[s];  // read here, with the rest, not at the end
         s_allowed[s] = 1;
         atomicAdd(&hist[e], 1);
     }
@@ -775,14 +790,14 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
             float tot = 0.0f;
             for (int j = 0; j < k; ++j) {
                 const int s = t * k + j;
-                tmp[j] = a.w0[s] * (s_allowed[s] ? 1.0f : 0.0f);
+                tmp[j] = s_w0[s] * (s_allowed[s] ? 1.0f : 0.0f);
                 tot = tot + tmp[j];
             }
             const float den = tot > 1e-8f ? tot : 1e-8f;
             const float keep = tot > 0.0f ? 1.0f : 0.0f;
             for (int j = 0; j < k; ++j) a.weights[t * k + j] = (tmp[j] * keep) / den;
         } else {
-            for (int j = 0; j < k; ++j) a.weights[t * k + j] = a.w0[t * k + j];
+            for (int j = 0; j < k; ++j) a.weights[t * k + j] = s_w0[t * k + j];
         }
     }
 }
