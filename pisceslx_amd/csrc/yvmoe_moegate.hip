@@ -17,6 +17,8 @@
 //   moegate_loss_kernel: the loss from the per-work-group sums, in a fixed order.
 #include <math.h>
 
+#include <algorithm>
+
 #include "yvmoe_internal.h"
 
 namespace yvmoe {
@@ -590,6 +592,293 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
     }
 }
 
+// One wavefront per token, for gates of at most 64 experts (lane e holds expert e): no
+// work-group barrier inside a token, so a work-group's wavefronts run their tokens
+// independently and the per-token latency chain (row loads, selection, prototype gathers)
+// overlaps across many tokens. Selection of the sel_k largest DG activations, with the same
+// result as moegate_token_kernel's:
+//   1. the row streams once for each lane's maximum (lane l holds entries 4 (64 j + l) .. + 3);
+//      the sel_k-th largest of the 64 lane maxima (ties to the lower lane) is a lower bound of
+//      the sel_k-th largest entry;
+//   2. the row streams again (from L2 / Infinity Cache) and the non-zero entries at or above the
+//      bound go to the wavefront's candidate list in LDS (typically a few dozen);
+//   3. if more than kWaveCand pass, the sel_k-th largest bit pattern T is found by bisection
+//      over the row (non-negative floats order like their bits), and the candidates become
+//      the entries above T plus the lowest-index entries equal to T;
+//   4. each candidate's rank in (value descending, index ascending) order places it.
+constexpr int kWaveTok = 4;     // wavefronts (tokens in flight) per work-group
+constexpr int kWaveCand = 256;  // candidate list per wavefront
+// Below this many tokens a wavefront per token cannot stream the rows fast enough (decode, 64
+// tokens: 110 us against 71 us for a work-group per token); the work-group form runs instead.
+constexpr int kWaveMinTokens = 1024;
+
+template <int NS>
+__device__ __forceinline__ float4 dg_load(const GateArgs& a, const float* row, int i4) {
+    float4 v = *(const float4*)(row + 4 * i4);
+#pragma unroll
+    for (int z = 1; z < NS; ++z) {
+        const float4 w = *(const float4*)(row + z * a.sstride + 4 * i4);
+        v.x += w.x;
+        v.y += w.y;
+        v.z += w.z;
+        v.w += w.w;
+    }
+    return v;
+}
+__device__ __forceinline__ unsigned relu_bits(float v) { return v > 0.f ? __float_as_uint(v) : 0u; }
+
+template <int NS>
+__global__ __launch_bounds__(64 * kWaveTok) void moegate_wave_kernel(GateArgs a) {
+    __shared__ float c_val[kWaveTok][kWaveCand];
+    __shared__ int c_idx[kWaveTok][kWaveCand];
+    __shared__ float s_sel[kWaveTok][kGateMaxSel];
+    __shared__ int s_sid[kWaveTok][kGateMaxSel];
+    __shared__ float s_hh[kWaveTok][256];
+    __shared__ unsigned s_cnt[kWaveTok];
+    __shared__ float s_part[kWaveTok][66];
+    extern __shared__ float s_eo[];  // the Expert-Oriented matrix [D][E], read by every token
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int E = a.E, D = a.D, K = a.sel_k;
+    const bool is_e = lane < E;
+    const bool hicl_on = (a.mask & YVMOE_HEAD_HICL) != 0;
+    const bool eo_on = (a.mask & YVMOE_HEAD_EO) != 0;
+    if (eo_on) {
+        for (int i = threadIdx.x; i < D * E; i += 64 * kWaveTok) s_eo[i] = a.eo_mat[i];
+        __syncthreads();
+    }
+    const int nj = a.dgdim / 256;  // 16-byte loads per lane per row
+    constexpr int BATCH = NS == 1 ? 8 : 4;
+    float acc_score = 0.f, acc_z = 0.f, acc_soft = 0.f;
+
+    for (int t = blockIdx.x * kWaveTok + wave; t < a.N; t += gridDim.x * kWaveTok) {
+        const float* hrow = a.heads + (long long)t * a.ld;
+        // ------------------------------------------------------------ head columns, biases
+        float gate = 0.f, got = 0.f, lk = 0.f, lv = 0.f, bias_e = 0.f, modal_e = 0.f;
+        if (is_e) {
+            gate = hrow[lane];
+            got = hrow[E + lane];
+            lk = hrow[2 * E + lane];
+            lv = hrow[3 * E + lane];
+#pragma unroll
+            for (int z = 1; z < NS; ++z) {
+                const float* hz = hrow + z * a.sstride;
+                gate += hz[lane];
+                got += hz[E + lane];
+                lk += hz[2 * E + lane];
+                lv += hz[3 * E + lane];
+            }
+            if (a.ebias != nullptr) bias_e = a.ebias[lane];
+            if (a.modal_id != nullptr) {
+                const int md = a.modal_id[t];
+                if (md >= 0 && md < a.nmod) modal_e = a.modal[lane * a.nmod + md];
+            }
+        }
+        if (eo_on) {
+            for (int d = lane; d < D; d += 64) {
+                float h1 = hrow[4 * E + d];
+#pragma unroll
+                for (int z = 1; z < NS; ++z) h1 += hrow[z * a.sstride + 4 * E + d];
+                s_hh[wave][d] = h1 / (1.f + expf(-h1));  // SiLU
+            }
+        }
+        // ------------------------------------------------------------ HiCL
+        float hicl = 0.f;
+        if (hicl_on) {
+            const float* drow = a.dg + (long long)t * a.ld;
+            // 1. lane maxima of the relu'd row, and the lower bound
+            unsigned m = 0u;
+            for (int j0 = 0; j0 < nj; j0 += BATCH) {
+                float4 v[BATCH];
+#pragma unroll
+                for (int b = 0; b < BATCH; ++b)
+                    if (j0 + b < nj) v[b] = dg_load<NS>(a, drow, (j0 + b) * 64 + lane);
+#pragma unroll
+                for (int b = 0; b < BATCH; ++b)
+                    if (j0 + b < nj)
+                        m = max(max(m, max(relu_bits(v[b].x), relu_bits(v[b].y))),
+                                max(relu_bits(v[b].z), relu_bits(v[b].w)));
+            }
+            unsigned r = 0u;
+#pragma unroll 8
+            for (int k = 0; k < 64; ++k) {
+                const unsigned g = (unsigned)__builtin_amdgcn_readlane((int)m, k);
+                r += (g > m || (g == m && k < lane)) ? 1u : 0u;
+            }
+            const int tl = __ffsll((long long)__ballot(r == (unsigned)(K - 1))) - 1;
+            const unsigned tlb = (unsigned)__shfl((int)m, tl);
+            // 2. candidates: non-zero entries at or above the bound
+            if (lane == 0) s_cnt[wave] = 0u;
+            for (int j0 = 0; j0 < nj; j0 += BATCH) {
+                float4 v[BATCH];
+#pragma unroll
+                for (int b = 0; b < BATCH; ++b)
+                    if (j0 + b < nj) v[b] = dg_load<NS>(a, drow, (j0 + b) * 64 + lane);
+#pragma unroll
+                for (int b = 0; b < BATCH; ++b) {
+                    if (j0 + b >= nj) continue;
+                    const float e4[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const unsigned u = relu_bits(e4[c]);
+                        if (u != 0u && u >= tlb) {
+                            const unsigned slot = atomicAdd(&s_cnt[wave], 1u);
+                            if (slot < (unsigned)kWaveCand) {
+                                c_val[wave][slot] = e4[c];
+                                c_idx[wave][slot] = 4 * ((j0 + b) * 64 + lane) + c;
+                            }
+                        }
+                    }
+                }
+            }
+            int C = (int)s_cnt[wave];
+            if (C > kWaveCand) {
+                // 3. too many: bisection for T = the K-th largest bit pattern among positive
+                // entries (cnt(x) = entries with bits >= x is non-increasing in x; T is the
+                // largest x with cnt(x) >= K; tlb satisfies it)
+                auto count_ge = [&](unsigned x) {
+                    unsigned n = 0u;
+                    for (int j = 0; j < nj; ++j) {
+                        const float4 v = dg_load<NS>(a, drow, j * 64 + lane);
+                        n += (relu_bits(v.x) >= x && v.x > 0.f) + (relu_bits(v.y) >= x && v.y > 0.f) +
+                             (relu_bits(v.z) >= x && v.z > 0.f) + (relu_bits(v.w) >= x && v.w > 0.f);
+                    }
+                    return (unsigned)__shfl((int)wave_prefix_sum(n), 63);
+                };
+                unsigned lo = tlb, hi = 0x7f800000u;  // cnt(lo) >= K; cnt(hi) < K (no inf)
+                while (hi - lo > 1u) {
+                    const unsigned mid = lo + (hi - lo) / 2u;
+                    if (count_ge(mid) >= (unsigned)K) lo = mid;
+                    else hi = mid;
+                }
+                const unsigned T = lo;
+                const unsigned need = (unsigned)K - count_ge(T + 1u);  // ties at T to take (>= 1)
+                // entries above T, then the first `need` entries equal to T in index order
+                // (index 4 (64 j + l) + c: j, then lane, then c)
+                unsigned taken = 0u;
+                int n = 0;
+                for (int j = 0; j < nj; ++j) {
+                    const float4 v = dg_load<NS>(a, drow, j * 64 + lane);
+                    const float e4[4] = {v.x, v.y, v.z, v.w};
+                    unsigned te = 0u;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) te += (relu_bits(e4[c]) == T && e4[c] > 0.f) ? 1u : 0u;
+                    const unsigned pre = wave_prefix_sum(te) - te;  // ties in lower lanes
+                    unsigned q = taken + pre;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const unsigned u = relu_bits(e4[c]);
+                        bool take = false;
+                        if (e4[c] > 0.f && u > T) take = true;
+                        else if (e4[c] > 0.f && u == T) take = q++ < need;
+                        const unsigned long long bal = __ballot(take);
+                        // lanes take slots in lane order for this c (positions of a fixed size)
+                        const int before = __builtin_popcountll(bal & ((1ull << lane) - 1ull));
+                        if (take) {
+                            c_val[wave][n + before] = e4[c];
+                            c_idx[wave][n + before] = 4 * (j * 64 + lane) + c;
+                        }
+                        n += __builtin_popcountll(bal);
+                    }
+                    taken += (unsigned)__shfl((int)(pre + te), 63);
+                }
+                C = n;  // == K
+            }
+            // 4. ranks (value descending, index ascending); ranks below K are kept
+            for (int i = lane; i < C; i += 64) {
+                const float mv = c_val[wave][i];
+                const int mi = c_idx[wave][i];
+                int rk = 0;
+                for (int k = 0; k < C; ++k) {
+                    const float cv = c_val[wave][k];
+                    rk += (cv > mv || (cv == mv && c_idx[wave][k] < mi)) ? 1 : 0;
+                }
+                if (rk < K) {
+                    s_sel[wave][rk] = mv;
+                    s_sid[wave][rk] = mi;
+                }
+            }
+            const int nsel = C < K ? C : K;
+            // F.normalize(p=2, eps=1e-12)
+            const float x = lane < nsel ? s_sel[wave][lane] : 0.f;
+            const float nrm = fmaxf(sqrtf(wave_sum(x * x)), 1e-12f);
+            if (lane < nsel) s_sel[wave][lane] = x / nrm;
+            if (is_e) {
+                const float* pcol = a.proto_t + lane;
+                for (int s0 = 0; s0 < nsel; s0 += 8) {
+                    float pv[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        pv[i] = s0 + i < nsel ? pcol[(long long)s_sid[wave][s0 + i] * E] : 0.f;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        if (s0 + i < nsel) hicl += s_sel[wave][s0 + i] * pv[i];
+                }
+            }
+        }
+        // ------------------------------------------------------------ Expert-Oriented
+        float eo = 0.f;
+        if (eo_on && is_e) {
+            for (int d = 0; d < D; ++d) eo += s_hh[wave][d] * s_eo[d * E + lane];
+        }
+        // ------------------------------------------------------------ SoftMoE, logits, loss
+        float soft = 0.f, soft_tot = 0.f;
+        if (a.mask & YVMOE_HEAD_SOFT) {
+            // torch.median: the lower middle value (rank, ties by index)
+            const int lkb = __float_as_int(lk);
+            unsigned rr = 0u;
+            for (int j = 0; j < E; ++j) {
+                const float xj = __int_as_float(__builtin_amdgcn_readlane(lkb, j));
+                rr += (xj < lk || (xj == lk && j < lane)) ? 1u : 0u;
+            }
+            const int ml = __ffsll((long long)__ballot(is_e && rr == (unsigned)((E - 1) / 2))) - 1;
+            const float med = __shfl(lk, ml);
+            const float mx = wave_max(is_e ? lv : -INFINITY);
+            const float ex = is_e ? expf(lv - mx) : 0.f;
+            const float se = wave_sum(ex);
+            float sv = is_e ? (1.f / (1.f + expf(-((lk - med) / a.soft_t)))) * (ex / se) : 0.f;
+            sv = sv / fmaxf(wave_sum(sv), a.soft_eps);
+            soft = sv;
+            soft_tot = wave_sum(sv);
+        }
+        float l = 0.f;
+        if (is_e) {
+            l = gate;
+            if (hicl_on) l = l + a.w_hicl * hicl;
+            if (a.mask & YVMOE_HEAD_GOT) l = l + a.w_got * got;
+            if (a.mask & YVMOE_HEAD_SOFT) l = l + a.w_soft * soft;
+            if (eo_on) l = l + a.w_eo * eo;
+            if (a.modal_id != nullptr) l = l + modal_e;
+            if (a.ebias != nullptr) l = l + bias_e;
+            l = l / a.temp;
+            a.logits[(long long)t * E + lane] = l;
+        }
+        const float lm = wave_max(is_e ? l : -INFINITY);
+        const float le = is_e ? expf(l - lm) : 0.f;
+        const float ls = wave_sum(le);
+        if (is_e) acc_score += le / ls;
+        const float z = wave_sum(is_e ? l * l : 0.f);
+        if (lane == 0) {
+            acc_z += z;
+            acc_soft += soft_tot;
+        }
+    }
+    // per-work-group loss sums: the wavefronts' in order
+    s_part[wave][lane] = acc_score;
+    if (lane == 0) {
+        s_part[wave][64] = acc_z;
+        s_part[wave][65] = acc_soft;
+    }
+    __syncthreads();
+    const int G = gridDim.x, g = blockIdx.x;
+    for (int c = threadIdx.x; c < E + 2; c += 64 * kWaveTok) {
+        const int col = c < E ? c : 64 + (c - E);
+        float sum = s_part[0][col];
+#pragma unroll
+        for (int w = 1; w < kWaveTok; ++w) sum += s_part[w][col];
+        a.part[(long long)c * G + g] = sum;
+    }
+}
+
 // loss = alpha · Σ_e (mean_n score - 1/E)² + capacity term + z_alpha · mean(logits²)
 //        + 0.01 · (mean_n Σ_e soft - budget)²   (gate.py:433-444, :556-610)
 // Column c of the per-work-group sums is summed by P threads (contiguous group ranges, 32
@@ -678,6 +967,7 @@ int moegate_launch(const void* x, int act, int N, const yvmoe_moegate* g, const 
     const int hoff = (g->heads & YVMOE_HEAD_HICL) ? g->dg_dim : 0;
     float* proj = (float*)(ws + w.proj);
     float* part = (float*)(ws + w.loss);
+    int groups = w.groups;  // work-groups whose loss sums the loss kernel reads
     if (N > 0) {
         const bool hicl = (g->heads & YVMOE_HEAD_HICL) != 0;
         int rc = dense_partials_launch(x, act, N, H, g->w_proj, P, proj, P, hicl ? g->dg_bias : nullptr,
@@ -721,6 +1011,15 @@ int moegate_launch(const void* x, int act, int N, const yvmoe_moegate* g, const 
             set_error("moegate: %d partial sums of the projection", a.nsplit);
             return YVMOE_ERR_SHAPE;
         }
+        if (E <= 64 && N >= kWaveMinTokens) {
+            // a wavefront per token; fewer work-groups than w.groups, so the loss kernel reads
+            // this many per-work-group sums
+            groups = std::min(ceil_div(N, kWaveTok), kGateGroups);
+            const size_t eo_bytes = (g->heads & YVMOE_HEAD_EO) ? (size_t)g->enc_dim * E * 4 : 0;
+            if (a.nsplit == 1) moegate_wave_kernel<1><<<groups, 64 * kWaveTok, eo_bytes, st>>>(a);
+            else moegate_wave_kernel<2><<<groups, 64 * kWaveTok, eo_bytes, st>>>(a);
+            YV_LAUNCH_CHECK("moegate_wave");
+        } else {
 #define YV_TOK(NS, J4) moegate_token_kernel<1024, NS, J4><<<w.groups, 1024, 0, st>>>(a)
         switch (j4 * 10 + a.nsplit) {
             case 11: YV_TOK(1, 1); break;
@@ -734,8 +1033,9 @@ int moegate_launch(const void* x, int act, int N, const yvmoe_moegate* g, const 
         }
 #undef YV_TOK
         YV_LAUNCH_CHECK("moegate_token");
+        }
     }
-    moegate_loss_kernel<<<1, 1024, 0, st>>>(part, w.groups, E, N, g->load_balance_alpha,
+    moegate_loss_kernel<<<1, 1024, 0, st>>>(part, groups, E, N, g->load_balance_alpha,
                                            g->z_loss_alpha, g->soft_budget, g->capacity_loss,
                                            (g->heads & YVMOE_HEAD_SOFT) ? 1 : 0, loss);
     YV_LAUNCH_CHECK("moegate_loss");
