@@ -595,19 +595,20 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
 // One wavefront per token, for gates of at most 64 experts (lane e holds expert e): no
 // work-group barrier inside a token, so a work-group's wavefronts run their tokens
 // independently and the per-token latency chain (row loads, selection, prototype gathers)
-// overlaps across many tokens. Selection of the sel_k largest DG activations, with the same
-// result as moegate_token_kernel's:
-//   1. the row streams once for each lane's maximum (lane l holds entries 4 (64 j + l) .. + 3);
-//      the sel_k-th largest of the 64 lane maxima (ties to the lower lane) is a lower bound of
-//      the sel_k-th largest entry;
-//   2. the row streams again (from L2 / Infinity Cache) and the non-zero entries at or above the
-//      bound go to the wavefront's candidate list in LDS (typically a few dozen);
-//   3. if more than kWaveCand pass, the sel_k-th largest bit pattern T is found by bisection
-//      over the row (non-negative floats order like their bits), and the candidates become
-//      the entries above T plus the lowest-index entries equal to T;
-//   4. each candidate's rank in (value descending, index ascending) order places it.
+// overlaps across many tokens. Selection of the sel_k largest DG activations in one pass over
+// the row (lane l holds entries 4 (64 j + l) .. + 3, j ascending): a candidate buffer in LDS
+// holds, in index order, every entry seen so far that can still be among the sel_k largest,
+// and a threshold thr admits only entries above it:
+//   - an entry is appended when its relu'd bit pattern exceeds thr (non-negative floats order
+//     like their bits; thr starts at 0, so the first entries admitted are the positive ones);
+//   - when the buffer would overflow it is compacted to exactly the sel_k largest so far (the
+//     entries above T, the sel_k-th largest bit pattern found by bisection, and the
+//     lowest-index entries equal to T), and thr becomes T: a later entry equal to T ranks
+//     after sel_k earlier ones (ties go to the lower index), so it cannot be kept;
+//   - after the row, one more compaction leaves the sel_k largest (or all positive entries if
+//     fewer), ranked in (value descending, index ascending) order.
 constexpr int kWaveTok = 4;     // wavefronts (tokens in flight) per work-group
-constexpr int kWaveCand = 256;  // candidate list per wavefront
+constexpr int kWaveCand = 512;  // candidate buffer per wavefront (compaction leaves <= 64)
 // Below this many tokens a wavefront per token cannot stream the rows fast enough (decode, 64
 // tokens: 110 us against 71 us for a work-group per token); the work-group form runs instead.
 constexpr int kWaveMinTokens = 1024;
@@ -627,9 +628,68 @@ __device__ __forceinline__ float4 dg_load(const GateArgs& a, const float* row, i
 }
 __device__ __forceinline__ unsigned relu_bits(float v) { return v > 0.f ? __float_as_uint(v) : 0u; }
 
+// Lanes below this one with the flag set in the wavefront mask b.
+__device__ __forceinline__ int lanes_below(unsigned long long b) {
+    return (int)__builtin_amdgcn_mbcnt_hi((unsigned)(b >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)b, 0u));
+}
+// Compacts the wavefront's candidate buffer (K <= n <= kWaveCand entries in index order, relu'd
+// bit patterns in cu) to its K largest (ties to the lower index), in index order; returns T,
+// the K-th largest bit pattern. The bisection for T runs on the entries held in registers.
+__device__ unsigned wave_compact(unsigned* cu, int* ci, int n, int K) {
+    constexpr int PER = kWaveCand / 64;
+    const int lane = threadIdx.x & 63;
+    unsigned r[PER];
+    unsigned mx = 0u;
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+        const int i = 64 * m + lane;
+        r[m] = i < n ? cu[i] : 0u;  // 0 never counts: every entry is positive
+        mx = max(mx, r[m]);
+    }
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) mx = max(mx, (unsigned)__shfl_xor((int)mx, o));
+    auto cnt_ge = [&](unsigned x) {
+        unsigned c = 0u;
+#pragma unroll
+        for (int m = 0; m < PER; ++m) c += r[m] >= x ? 1u : 0u;
+        return (unsigned)wave_sum((float)c);  // counts <= kWaveCand: exact in fp32
+    };
+    unsigned lo = 1u, hi = mx + 1u;  // cnt(lo) = n >= K, cnt(hi) = 0 < K
+    while (hi - lo > 1u) {
+        const unsigned mid = lo + (hi - lo) / 2u;
+        if (cnt_ge(mid) >= (unsigned)K) lo = mid;
+        else hi = mid;
+    }
+    const unsigned T = lo;
+    const unsigned need = (unsigned)K - cnt_ge(T + 1u);  // entries equal to T to keep (>= 1)
+    // stable compaction, 64 entries at a time (kept entries move to lower or equal positions,
+    // and every entry was read into registers above)
+    int x[PER];
+#pragma unroll
+    for (int m = 0; m < PER; ++m) x[m] = 64 * m + lane < n ? ci[64 * m + lane] : 0;
+    unsigned ties = 0u;
+    int w = 0;
+#pragma unroll
+    for (int m = 0; m < PER; ++m) {
+        const bool tie = r[m] == T;
+        const unsigned long long tb = __ballot(tie);
+        const unsigned trank = ties + (unsigned)lanes_below(tb);
+        const bool keep = r[m] > T || (tie && trank < need);
+        const unsigned long long kb = __ballot(keep);
+        if (keep) {
+            const int pos = w + lanes_below(kb);
+            cu[pos] = r[m];
+            ci[pos] = x[m];
+        }
+        ties += (unsigned)__popcll(tb);
+        w += __popcll(kb);
+    }
+    return T;
+}
+
 template <int NS>
 __global__ __launch_bounds__(64 * kWaveTok) void moegate_wave_kernel(GateArgs a) {
-    __shared__ float c_val[kWaveTok][kWaveCand];
+    __shared__ unsigned c_bits[kWaveTok][kWaveCand];
     __shared__ int c_idx[kWaveTok][kWaveCand];
     __shared__ float s_sel[kWaveTok][kGateMaxSel];
     __shared__ int s_sid[kWaveTok][kGateMaxSel];
@@ -685,29 +745,8 @@ __global__ __launch_bounds__(64 * kWaveTok) void moegate_wave_kernel(GateArgs a)
         float hicl = 0.f;
         if (hicl_on) {
             const float* drow = a.dg + (long long)t * a.ld;
-            // 1. lane maxima of the relu'd row, and the lower bound
-            unsigned m = 0u;
-            for (int j0 = 0; j0 < nj; j0 += BATCH) {
-                float4 v[BATCH];
-#pragma unroll
-                for (int b = 0; b < BATCH; ++b)
-                    if (j0 + b < nj) v[b] = dg_load<NS>(a, drow, (j0 + b) * 64 + lane);
-#pragma unroll
-                for (int b = 0; b < BATCH; ++b)
-                    if (j0 + b < nj)
-                        m = max(max(m, max(relu_bits(v[b].x), relu_bits(v[b].y))),
-                                max(relu_bits(v[b].z), relu_bits(v[b].w)));
-            }
-            unsigned r = 0u;
-#pragma unroll 8
-            for (int k = 0; k < 64; ++k) {
-                const unsigned g = (unsigned)__builtin_amdgcn_readlane((int)m, k);
-                r += (g > m || (g == m && k < lane)) ? 1u : 0u;
-            }
-            const int tl = __ffsll((long long)__ballot(r == (unsigned)(K - 1))) - 1;
-            const unsigned tlb = (unsigned)__shfl((int)m, tl);
-            // 2. candidates: non-zero entries at or above the bound
-            if (lane == 0) s_cnt[wave] = 0u;
+            unsigned thr = 0u;
+            int n = 0;
             for (int j0 = 0; j0 < nj; j0 += BATCH) {
                 float4 v[BATCH];
 #pragma unroll
@@ -716,88 +755,56 @@ __global__ __launch_bounds__(64 * kWaveTok) void moegate_wave_kernel(GateArgs a)
 #pragma unroll
                 for (int b = 0; b < BATCH; ++b) {
                     if (j0 + b >= nj) continue;
-                    const float e4[4] = {v[b].x, v[b].y, v[b].z, v[b].w};
+                    const unsigned u[4] = {relu_bits(v[b].x), relu_bits(v[b].y), relu_bits(v[b].z), relu_bits(v[b].w)};
+                    unsigned long long bl[4];
+                    int tot = 0;
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        const unsigned u = relu_bits(e4[c]);
-                        if (u != 0u && u >= tlb) {
-                            const unsigned slot = atomicAdd(&s_cnt[wave], 1u);
-                            if (slot < (unsigned)kWaveCand) {
-                                c_val[wave][slot] = e4[c];
-                                c_idx[wave][slot] = 4 * ((j0 + b) * 64 + lane) + c;
-                            }
+                        bl[c] = __ballot(u[c] > thr);
+                        tot += __popcll(bl[c]);
+                    }
+                    if (tot == 0) continue;  // wave-uniform
+                    if (n + tot > kWaveCand) {
+                        thr = wave_compact(c_bits[wave], c_idx[wave], n, K);
+                        n = K;
+                        tot = 0;
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            bl[c] = __ballot(u[c] > thr);
+                            tot += __popcll(bl[c]);
                         }
                     }
-                }
-            }
-            int C = (int)s_cnt[wave];
-            if (C > kWaveCand) {
-                // 3. too many: bisection for T = the K-th largest bit pattern among positive
-                // entries (cnt(x) = entries with bits >= x is non-increasing in x; T is the
-                // largest x with cnt(x) >= K; tlb satisfies it)
-                auto count_ge = [&](unsigned x) {
-                    unsigned n = 0u;
-                    for (int j = 0; j < nj; ++j) {
-                        const float4 v = dg_load<NS>(a, drow, j * 64 + lane);
-                        n += (relu_bits(v.x) >= x && v.x > 0.f) + (relu_bits(v.y) >= x && v.y > 0.f) +
-                             (relu_bits(v.z) >= x && v.z > 0.f) + (relu_bits(v.w) >= x && v.w > 0.f);
-                    }
-                    return (unsigned)__shfl((int)wave_prefix_sum(n), 63);
-                };
-                unsigned lo = tlb, hi = 0x7f800000u;  // cnt(lo) >= K; cnt(hi) < K (no inf)
-                while (hi - lo > 1u) {
-                    const unsigned mid = lo + (hi - lo) / 2u;
-                    if (count_ge(mid) >= (unsigned)K) lo = mid;
-                    else hi = mid;
-                }
-                const unsigned T = lo;
-                const unsigned need = (unsigned)K - count_ge(T + 1u);  // ties at T to take (>= 1)
-                // entries above T, then the first `need` entries equal to T in index order
-                // (index 4 (64 j + l) + c: j, then lane, then c)
-                unsigned taken = 0u;
-                int n = 0;
-                for (int j = 0; j < nj; ++j) {
-                    const float4 v = dg_load<NS>(a, drow, j * 64 + lane);
-                    const float e4[4] = {v.x, v.y, v.z, v.w};
-                    unsigned te = 0u;
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) te += (relu_bits(e4[c]) == T && e4[c] > 0.f) ? 1u : 0u;
-                    const unsigned pre = wave_prefix_sum(te) - te;  // ties in lower lanes
-                    unsigned q = taken + pre;
+                    // this lane's entries follow every entry of the lower lanes (index order)
+                    int pos = n + lanes_below(bl[0]) + lanes_below(bl[1]) + lanes_below(bl[2]) +
+                              lanes_below(bl[3]);
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        const unsigned u = relu_bits(e4[c]);
-                        bool take = false;
-                        if (e4[c] > 0.f && u > T) take = true;
-                        else if (e4[c] > 0.f && u == T) take = q++ < need;
-                        const unsigned long long bal = __ballot(take);
-                        // lanes take slots in lane order for this c (positions of a fixed size)
-                        const int before = __builtin_popcountll(bal & ((1ull << lane) - 1ull));
-                        if (take) {
-                            c_val[wave][n + before] = e4[c];
-                            c_idx[wave][n + before] = 4 * (j * 64 + lane) + c;
+                        if (u[c] > thr) {
+                            c_bits[wave][pos] = u[c];
+                            c_idx[wave][pos] = 4 * ((j0 + b) * 64 + lane) + c;
+                            ++pos;
                         }
-                        n += __builtin_popcountll(bal);
                     }
-                    taken += (unsigned)__shfl((int)(pre + te), 63);
+                    n += tot;
                 }
-                C = n;  // == K
             }
-            // 4. ranks (value descending, index ascending); ranks below K are kept
-            for (int i = lane; i < C; i += 64) {
-                const float mv = c_val[wave][i];
-                const int mi = c_idx[wave][i];
+            if (n > K) {
+                wave_compact(c_bits[wave], c_idx[wave], n, K);
+                n = K;
+            }
+            const int C = n;
+            // ranks (value descending; the buffer is in index order, so ties by position)
+            if (lane < C) {
+                const unsigned mv = c_bits[wave][lane];
                 int rk = 0;
                 for (int k = 0; k < C; ++k) {
-                    const float cv = c_val[wave][k];
-                    rk += (cv > mv || (cv == mv && c_idx[wave][k] < mi)) ? 1 : 0;
+                    const unsigned cv = c_bits[wave][k];
+                    rk += (cv > mv || (cv == mv && k < lane)) ? 1 : 0;
                 }
-                if (rk < K) {
-                    s_sel[wave][rk] = mv;
-                    s_sid[wave][rk] = mi;
-                }
+                s_sel[wave][rk] = __uint_as_float(mv);
+                s_sid[wave][rk] = c_idx[wave][lane];
             }
-            const int nsel = C < K ? C : K;
+            const int nsel = C;
             // F.normalize(p=2, eps=1e-12)
             const float x = lane < nsel ? s_sel[wave][lane] : 0.f;
             const float nrm = fmaxf(sqrtf(wave_sum(x * x)), 1e-12f);
