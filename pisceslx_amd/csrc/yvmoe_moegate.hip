@@ -1018,13 +1018,13 @@ int moegate_launch(const void* x, int act, int N, const yvmoe_moegate* g, const 
             set_error("moegate: %d partial sums of the projection", a.nsplit);
             return YVMOE_ERR_SHAPE;
         }
-        if (E <= 64 && N >= kWaveMinTokens) {
+        if (E <= 64 && N >= kWaveMinTokens && a.nsplit == 1) {
             // a wavefront per token; fewer work-groups than w.groups, so the loss kernel reads
             // this many per-work-group sums
             groups = std::min(ceil_div(N, kWaveTok), kGateGroups);
             const size_t eo_bytes = (g->heads & YVMOE_HEAD_EO) ? (size_t)g->enc_dim * E * 4 : 0;
-            if (a.nsplit == 1) moegate_wave_kernel<1><<<groups, 64 * kWaveTok, eo_bytes, st>>>(a);
-            else moegate_wave_kernel<2><<<groups, 64 * kWaveTok, eo_bytes, st>>>(a);
+            // (at these sizes the projection is never split: one partial sum)
+            moegate_wave_kernel<1><<<groups, 64 * kWaveTok, eo_bytes, st>>>(a);
             YV_LAUNCH_CHECK("moegate_wave");
         } else {
 #define YV_TOK(NS, J4) moegate_token_kernel<1024, NS, J4><<<w.groups, 1024, 0, st>>>(a)

@@ -180,3 +180,52 @@ def test_path_moe_stage_cache(cuda):
     y = torch.randn(1, 7, H, generator=gen).to(torch.bfloat16).cuda()
     assert torch.equal(g(y)[1], g2(y)[1])
     assert fresh[0] is not None
+
+
+# Batches of 1024 tokens and more take the wavefront-per-token form (a gate of at most 64
+# experts): the same checks, and the DG selection cases that reach its buffer compaction
+# (entries tied at the threshold, more candidates than the buffer holds, few positives).
+@pytest.mark.parametrize("B,S,H,E,k,scale", [
+    (4, 300, 1024, 64, 6, False),
+    (2, 520, 2048, 32, 4, True),
+])
+def test_moegate_wave_form_matches_oracle(cuda, oracle, B, S, H, E, k, scale):
+    g = _gate(H, E, k, scale_heads=scale, seed=H + E + 1)
+    x = torch.randn(B, S, H, generator=torch.Generator().manual_seed(7)).to(torch.bfloat16).cuda()
+    _check(g, x, oracle)
+
+
+def test_moegate_wave_form_dg_selection_cases(cuda, oracle):
+    H, E = 1024, 16                          # DG width 4096
+    g = _gate(H, E, 2, scale_heads=True, seed=9)
+    dg = g.hicl_dg_encoder
+    x = torch.randn(2, 530, H, generator=torch.Generator().manual_seed(8)).to(torch.bfloat16).cuda()
+    with torch.no_grad():                    # ~1500 entries tie at the 32nd place
+        dg.dg_proj.weight.zero_()
+        b = torch.full((dg.dg_dim,), -1.0)
+        b[torch.arange(1, 1001, 2)] = 1.0
+        b[torch.arange(2, 3002, 3)] = 1.0
+        b[[17, 900, 40, 3]] = torch.tensor([2.0, 3.0, 2.5, 2.0])
+        dg.dg_bias.copy_(b)
+    _check(g, x, oracle)
+    with torch.no_grad():                    # every activation equal: the 32 lowest indices
+        dg.dg_bias.fill_(0.5)
+    _check(g, x, oracle)
+    with torch.no_grad():                    # values rising with the index: every entry enters
+        dg.dg_bias.copy_(torch.linspace(0.01, 2.0, dg.dg_dim))
+    _check(g, x, oracle)
+    with torch.no_grad():                    # values falling with the index: the first 32 stay
+        dg.dg_bias.copy_(torch.linspace(2.0, 0.01, dg.dg_dim))
+    _check(g, x, oracle)
+    with torch.no_grad():                    # 10 positive activations only
+        b = torch.full((dg.dg_dim,), -1.0)
+        b[torch.arange(0, 1000, 100)] = torch.linspace(0.5, 1.5, 10)
+        dg.dg_bias.copy_(b)
+    _check(g, x, oracle)
+    with torch.no_grad():                    # random weights, a five-way tie at the last places
+        dg.dg_proj.weight.normal_(0.0, 0.02)
+        b = torch.full((dg.dg_dim,), -3.0)
+        b[torch.arange(3, 93, 3)] = 4.0
+        b[[700, 5, 1000, 11, 400]] = 3.5
+        dg.dg_bias.copy_(b)
+    _check(g, x, oracle)
