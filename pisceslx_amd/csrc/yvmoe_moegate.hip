@@ -694,7 +694,6 @@ __global__ __launch_bounds__(64 * kWaveTok) void moegate_wave_kernel(GateArgs a)
     __shared__ float s_sel[kWaveTok][kGateMaxSel];
     __shared__ int s_sid[kWaveTok][kGateMaxSel];
     __shared__ float s_hh[kWaveTok][256];
-    __shared__ unsigned s_cnt[kWaveTok];
     __shared__ float s_part[kWaveTok][66];
     extern __shared__ float s_eo[];  // the Expert-Oriented matrix [D][E], read by every token
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;

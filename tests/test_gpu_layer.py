@@ -166,6 +166,23 @@ def test_tiled_folded_remainders(cuda, oracle, fmt, hidden):
     assert routing.counts.cpu().tolist() == counts
 
 
+def _shared_spec(fmt_name, S):
+    from pisceslx_amd import _lib
+    from pisceslx_amd.workloads import LayerSpec
+    fmt = {"int8": _lib.W_INT8, "int4": _lib.W_INT4, "fp8": _lib.W_FP8, "bf16": _lib.W_BF16}[fmt_name]
+    return LayerSpec(f"shared_{fmt_name}_s{S}", 1024, 512, 16, 4, S, fmt, torch.bfloat16)
+
+
+@pytest.mark.parametrize("fmt,S,n", [("int8", 2, 23), ("fp8", 3, 5), ("int4", 1, 64),
+                                     ("bf16", 2, 17)])
+def test_decode_shared_expert_segments(cuda, oracle, fmt, S, n):
+    """Decode sizes (the streaming form, 16-row tiles): the shared experts' segments of the
+    tile table (rows N*k + s*N, tiles cut at each segment end) for every weight format, 1-3
+    shared experts and batches that end inside a 16-row tile."""
+    w = make_workload(_shared_spec(fmt, S), device="cuda", lengths=[n])
+    _run_and_check(oracle, w, label=f"shared segments {fmt} S={S} N={n}")
+
+
 def test_forward_is_deterministic(cuda, oracle):
     w = make_workload("cfg3", device="cuda", n_tokens=700)
     st = router_state(w)
