@@ -1287,6 +1287,16 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
         }
     };
     float tmp[VEC];
+    // the loads that do not wait on the routing (the first KC shared rows and the skip row) go
+    // out first, so they travel with the routed rows instead of after them
+    Raw qs[KC], qk{};
+#pragma unroll
+    for (int i = 0; i < KC; ++i)
+        if (i < S) qs[i] = raw_load((long long)N * k + (long long)i * N + t);
+    if (skip != nullptr) {
+        if constexpr (ACT == YVMOE_ACT_BF16) qk = *(const uint4*)((const unsigned short*)skip + (long long)t * H + h);
+        else qk = *(const float4*)((const float*)skip + (long long)t * H + h);
+    }
     // a slot without a position (pos < 0: an expert id outside [0, E) handed to the dispatch
     // entry) has no expert output and adds nothing
     for (int j0 = 0; j0 < k; j0 += KC) {
@@ -1317,7 +1327,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
         Raw q[KC];
 #pragma unroll
         for (int i = 0; i < KC; ++i)
-            if (s0 + i < S) q[i] = raw_load((long long)N * k + (long long)(s0 + i) * N + t);
+            if (s0 + i < S) q[i] = s0 == 0 ? qs[i] : raw_load((long long)N * k + (long long)(s0 + i) * N + t);
 #pragma unroll
         for (int i = 0; i < KC; ++i) {
             if (s0 + i < S) {
@@ -1336,7 +1346,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
     for (int v = 0; v < VEC; ++v) o[v] = rnd<ACT>(rnd<ACT>(acc[v]) + sh[v]);
     if (skip != nullptr) {
         if constexpr (ACT == YVMOE_ACT_BF16) {
-            const uint4 q = *(const uint4*)((const unsigned short*)skip + (long long)t * H + h);
+            const uint4 q = qk;
             const unsigned u[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -1344,7 +1354,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const void* __restrict__ y
                 o[2 * i + 1] = rnd<ACT>(o[2 * i + 1] + rnd<ACT>(0.1f * __uint_as_float(u[i] & 0xffff0000u)));
             }
         } else {
-            const float4 q = *(const float4*)((const float*)skip + (long long)t * H + h);
+            const float4 q = qk;
             o[0] = o[0] + 0.1f * q.x;
             o[1] = o[1] + 0.1f * q.y;
             o[2] = o[2] + 0.1f * q.z;
