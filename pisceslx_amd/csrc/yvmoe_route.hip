@@ -730,6 +730,19 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
             const int n = s_off[e + 1] - s_off[e];
             if (n <= cap) continue;
             const int off = s_off[e];
+            if (n <= 64) {
+                // lane i holds slot i's probability; slot j's is broadcast from lane j (no LDS
+                // round trip per comparison)
+                const int si = lane < n ? s_perm[off + lane] : 0;
+                const float pi = lane < n ? s_topp[si] : 0.0f;
+                int rank = 0;
+                for (int j = 0; j < n; ++j) {
+                    const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pi), j));
+                    rank += (pj > pi || (pj == pi && j < lane)) ? 1 : 0;
+                }
+                if (lane < n && rank >= cap) s_allowed[si] = 0;
+                continue;
+            }
             for (int i = lane; i < n; i += 64) {
                 const int si = s_perm[off + i];
                 const float pi = s_topp[si];
