@@ -36,6 +36,9 @@
 #ifndef YV_NB2
 #define YV_NB2 1  // column blocks per wavefront, streaming down projection (1 measured best)
 #endif
+#ifndef YV_DPF
+#define YV_DPF true  // dense streaming with 64-row tiles: weights one chunk ahead
+#endif
 #ifndef YV_U1
 #define YV_U1 4  // k-steps per staged chunk, streaming gate/up
 #endif
@@ -469,7 +472,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
 // that measured closest to the HBM ceiling), reading activation fragments from LDS. More
 // column blocks per wavefront put more weight bytes in flight per activation chunk and per
 // barrier.
-template <int WF, int EPI, int U, int MAXRB, int NB>
+template <int WF, int EPI, int U, int MAXRB, int NB, bool PF = false>
 __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int cgroup, int kz,
                                             uint4 (&As)[2][16 * MAXRB * (U * 8 + 1)]) {
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
@@ -565,6 +568,73 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
             }
         }
     };
+    if constexpr (PF) {
+        // Weights one chunk ahead in a second register set (for launches of few work-groups
+        // per CU, whose weight bytes in flight would otherwise be one chunk per wavefront): the
+        // loop is unrolled by two so the sets alternate without copies; every load and staging
+        // step is unconditional (clamped to the last chunk, in bounds, never used), and the
+        // MFMAs of k-steps past the end are skipped.
+        typename BL::Raw bw2[NB][U];
+        float sg2[NB][U];
+        auto load_into = [&](int c, typename BL::Raw (&w)[NB][U], float (&sc)[NB][U]) {
+            const int ks0 = c * U;
+#pragma unroll
+            for (int b = 0; b < NB; ++b) {
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const int ks = min(ks0 + u, nks - 1);
+                    BL::load_blk_nt(w[b][u], bptr[b], ks);
+                    if constexpr (GROUPED) sc[b][u] = b_scale<WF>(S, s_off, n[b], p.K, kbeg + ks * 64);
+                    else sc[b][u] = scl[b];
+                }
+            }
+        };
+        auto body = [&](int c, typename BL::Raw (&cw)[NB][U], float (&cs)[NB][U],
+                        typename BL::Raw (&nw)[NB][U], float (&ns)[NB][U]) {
+            // the staging loads first: the wait for them before their LDS store (the counter
+            // is in order) then leaves the next chunk's weights in flight
+            uint4 nx[PER_THREAD];
+            stage_load(min(c + 1, nchunks - 1), nx);
+            load_into(min(c + 1, nchunks - 1), nw, ns);
+            const uint4* arow = &As[c & 1][(lane & 15) * ROW_U4 + (lane >> 4) * 2];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                if (c * U + u < nks) {
+                    Frag16 af[MAXRB];
+#pragma unroll
+                    for (int rb = 0; rb < MAXRB; ++rb) {
+                        af[rb].u[0] = arow[rb * 16 * ROW_U4 + u * 8];
+                        af[rb].u[1] = arow[rb * 16 * ROW_U4 + u * 8 + 1];
+                    }
+#pragma unroll
+                    for (int b = 0; b < NB; ++b) {
+                        Frag16 bf;
+                        BL::cvt(cw[b][u], cs[b][u], bf);
+#pragma unroll
+                        for (int rb = 0; rb < MAXRB; ++rb) {
+                            if (rb < nrb) {
+                                acc[b][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[rb].v[0], bf.v[0], acc[b][rb], 0, 0, 0);
+                                acc[b][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[rb].v[1], bf.v[1], acc[b][rb], 0, 0, 0);
+                            }
+                        }
+                    }
+                }
+            }
+            stage_store((c + 1) & 1, nx);
+            __syncthreads();
+        };
+        load_into(0, bw, sg);
+        {
+            uint4 v[PER_THREAD];
+            stage_load(0, v);
+            stage_store(0, v);
+        }
+        __syncthreads();
+        for (int c = 0; c < nchunks; c += 2) {
+            body(c, bw, sg, bw2, sg2);
+            body(c + 1, bw2, sg2, bw, sg);
+        }
+    } else {
     // chunk 0's weight loads go out before the activation staging, which waits on the row map
     // and the activation loads: the first weights are in flight during that chain
     load_w(0);
@@ -609,6 +679,7 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
         }
         if (c + 1 < nchunks) stage_store((c + 1) & 1, nxt);
         __syncthreads();
+    }
     }
 
     if constexpr (SWIGLU) {
@@ -675,7 +746,7 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
 // contiguous ranges, one per XCD: the tiles that share weights (the 16-row tiles of a shared
 // expert, which all read the same columns) then run together on one XCD and fetch those
 // weights from HBM once into its L2 instead of once per tile.
-template <int WF, int EPI, int U, int MAXRB, int NB>
+template <int WF, int EPI, int U, int MAXRB, int NB, bool PF = false>
 __global__ __launch_bounds__(256) void gemm_stream_kernel(GemmParams p, int ngroups, int nsplit) {
     __shared__ uint4 As[2][16 * MAXRB * (U * 8 + 1)];
     const int nt = p.tile_seg == nullptr ? (p.nrows + 16 * MAXRB - 1) / (16 * MAXRB) : *p.ntiles;
@@ -686,7 +757,7 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(GemmParams p, int ngro
     const int item = (blockIdx.x % 8) * per_xcd + local;
     if (item >= nitems) return;
     const int rest = item / nt;  // tile fastest, then column group, then K split
-    stream_item<WF, EPI, U, MAXRB, NB>(p, item % nt, rest % ngroups, rest / ngroups, As);
+    stream_item<WF, EPI, U, MAXRB, NB, PF>(p, item % nt, rest % ngroups, rest / ngroups, As);
 }
 
 // ------------------------------------------------------------------ bf16, LDS-tiled form
@@ -1391,13 +1462,13 @@ __global__ __launch_bounds__(256) void reduce_splits_kernel(const float* __restr
 
 // Streaming (decode) form: one (tile, column group) item per work-group; NB 16-column
 // blocks per wavefront.
-template <int EPI, int U, int NB, int MAXRB = 1>
+template <int EPI, int U, int NB, int MAXRB = 1, bool PF = false>
 int stream_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, const char* name,
                     int nsplit = 1) {
     const int ngroups = (EPI == EPI_SWIGLU) ? ceil_div(p.ncols, 32 * NB) : ceil_div(p.ncols, 64 * NB);
     const long long items = 8LL * ceil_div(ntiles_max * ngroups * nsplit, 8);
     if (items <= 0) return YVMOE_OK;
-#define YV_ST(WFV) gemm_stream_kernel<WFV, EPI, U, MAXRB, NB><<<(unsigned)items, 256, 0, st>>>(p, ngroups, nsplit)
+#define YV_ST(WFV) gemm_stream_kernel<WFV, EPI, U, MAXRB, NB, PF><<<(unsigned)items, 256, 0, st>>>(p, ngroups, nsplit)
     if constexpr (EPI == EPI_F32) {  // dense fp32 output: bf16 weights only
         if (wf != YVMOE_W_BF16) {
             set_error("%s: fp32-output streaming form needs bf16 weights", name);
@@ -1574,7 +1645,7 @@ int dense_partials_launch(const void* x, int act, int N, int K, const void* w, i
     if (dense_tiled(act, N, ncols, K)) return tile_dispatch<EPI_F32>(YVMOE_W_BF16, p, ceil_div(N, TBM), st, name);
     if (dense_streamed(act, N, ncols, K)) {
         if (N <= 16) return stream_dispatch<EPI_F32, 4, 1, 1>(YVMOE_W_BF16, p, 1, st, name, ks);
-        return stream_dispatch<EPI_F32, 2, 1, 4>(YVMOE_W_BF16, p, 1, st, name, ks);
+        return stream_dispatch<EPI_F32, 2, 1, 4, YV_DPF>(YVMOE_W_BF16, p, 1, st, name, ks);
     }
     const int wf = (act == YVMOE_ACT_F32) ? YVMOE_W_F32 : YVMOE_W_BF16;
     return gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), (ncols % 32 == 0) ? 2 : 1, ks,
