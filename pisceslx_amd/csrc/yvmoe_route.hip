@@ -584,14 +584,17 @@ struct SmallRouteArgs {
     TileTable tiles;  // tiles.seg == nullptr: no tile table
 };
 
-// Inclusive prefix sum over the 64 lanes of a wavefront.
+// Inclusive prefix sum over the 64 lanes of a wavefront, by DPP moves (no LDS permute round
+// trips): shifts right by 1, 2, 4 and 8 lanes inside each row of 16 (lanes without a source
+// add 0), then lane 15 of rows 0 and 2 into rows 1 and 3 (row_bcast:15) and lane 31 into rows
+// 2 and 3 (row_bcast:31).
 __device__ __forceinline__ int wave_incl_scan(int v) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int u = __shfl_up(v, o, 64);
-        if (lane >= o) v += u;
-    }
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
     return v;
 }
 
@@ -606,6 +609,8 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
     __shared__ float s_topp[kSmallSlots];
     __shared__ float s_w0[kSmallSlots];
     __shared__ float s_score[kSmallRouteTok];
+    __shared__ float s_tpos[kSmallSlots];          // probability of the slot at each position
+    __shared__ unsigned char s_epos[kSmallSlots];  // expert of each position
     __shared__ int s_cap;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -718,46 +723,34 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
         a.perm[p] = s;
         a.pos[s] = p;
         s_perm[p] = (unsigned short)s;
+        s_tpos[p] = s_topp[s];
+        s_epos[p] = (unsigned char)e;
     }
     __syncthreads();
 
-    // capacity trim: a wavefront per over-full expert; slot i (token order) is kept iff
-    // #{j: p_j > p_i} + #{j < i: p_j == p_i} < cap. The last wave builds the tile table.
+    // capacity trim, every position at once: the slot at position p of an over-full expert's
+    // segment [off, off + n) (positions in token order: the scatter is stable) is kept iff
+    // #{j: p_j > p_p} + #{j before p: p_j == p_p} < cap. The last wavefront builds the tile
+    // table meanwhile (it holds positions only when there are more than 960 slots).
     const int cap = s_cap;
     if (cap >= 0) {
-        for (int e = wave; e < E; e += 15) {
-            if (wave == 15) break;
-            const int n = s_off[e + 1] - s_off[e];
+        for (int q = tid; q < nslots; q += 1024) {
+            const int e = s_epos[q];
+            const int off = s_off[e], n = s_off[e + 1] - off;
             if (n <= cap) continue;
-            const int off = s_off[e];
-            if (n <= 64) {
-                // lane i holds slot i's probability; slot j's is broadcast from lane j (no LDS
-                // round trip per comparison)
-                const int si = lane < n ? s_perm[off + lane] : 0;
-                const float pi = lane < n ? s_topp[si] : 0.0f;
-                int rank = 0;
-                for (int j = 0; j < n; ++j) {
-                    const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pi), j));
-                    rank += (pj > pi || (pj == pi && j < lane)) ? 1 : 0;
-                }
-                if (lane < n && rank >= cap) s_allowed[si] = 0;
-                continue;
+            const float tq = s_tpos[q];
+            int rank = 0;
+            for (int j = 0; j < n; ++j) {
+                const float tj = s_tpos[off + j];
+                rank += (tj > tq || (tj == tq && off + j < q)) ? 1 : 0;
             }
-            for (int i = lane; i < n; i += 64) {
-                const int si = s_perm[off + i];
-                const float pi = s_topp[si];
-                int rank = 0;
-                for (int j = 0; j < n; ++j) {
-                    const float pj = s_topp[s_perm[off + j]];
-                    rank += (pj > pi || (pj == pi && j < i)) ? 1 : 0;
-                }
-                if (rank >= cap) s_allowed[si] = 0;
-            }
+            if (rank >= cap) s_allowed[s_perm[q]] = 0;
         }
     }
     if (wave == 15 && a.tiles.seg != nullptr) {
         // tile table of the expert GEMMs (build_tiles_kernel): lane l owns segments 5l .. 5l + 4
         const int S = a.tiles.S, tr = a.tiles.tile_rows, fold = a.tiles.fold;
+        const int lg = 31 - __builtin_clz(tr);  // tile heights are powers of two (host-checked)
         const int nseg = E + S;
         int s0[5], nt[5], loc = 0;
 #pragma unroll
@@ -776,7 +769,8 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
                 if (sg == nseg - 1) a.tiles.seg[nseg] = e_;
             }
             s0[i] = b;
-            nt[i] = seg_tiles(e_ - b, tr, fold);
+            const int rows = e_ - b, full = rows >> lg, rem = rows & (tr - 1);
+            nt[i] = full + ((rem > 0 && !(full > 0 && rem <= fold)) ? 1 : 0);  // seg_tiles
             loc += nt[i];
         }
         const int incl = wave_incl_scan(loc);
@@ -923,7 +917,11 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
         a.perm = out->perm;
         a.pos = out->pos;
         a.cap_out = out->capacity;
-        if (tiles) a.tiles = *tiles;
+        if (tiles) {
+            YV_REQUIRE(tiles->tile_rows > 0 && (tiles->tile_rows & (tiles->tile_rows - 1)) == 0,
+                       YVMOE_ERR_ARG, "tile rows %d not a power of two", tiles->tile_rows);
+            a.tiles = *tiles;
+        }
         route_small_kernel<<<1, 1024, 0, st>>>(a);
         YV_LAUNCH_CHECK("route_small");
         return YVMOE_OK;
