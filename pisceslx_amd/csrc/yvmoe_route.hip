@@ -26,9 +26,7 @@ namespace {
 
 constexpr int kLanes = 16;  // lanes cooperating on one token
 
-__device__ __forceinline__ float yv_expf(float x) {
-    if (!(x >= -86.0f)) return 0.0f;
-    if (x > 88.0f) return __builtin_huge_valf();
+__device__ __forceinline__ float yv_expf_core(float x) {
     float fn = rintf(x * 1.44269504088896341f);
     int n = (int)fn;
     float r = x - fn * 0.693359375f;
@@ -44,8 +42,12 @@ __device__ __forceinline__ float yv_expf(float x) {
     return p * __uint_as_float((unsigned)(n + 127) << 23);
 }
 
-__device__ __forceinline__ bool better(float v1, int e1, float v2, int e2) {
-    return v1 > v2 || (v1 == v2 && e1 < e2);
+__device__ __forceinline__ float yv_expf(float x) {
+    // the out-of-range results by selects rather than early returns (no branches); the clamped
+    // argument keeps the core's arithmetic finite, and its result is discarded for those inputs
+    const float xc = fminf(fmaxf(x, -86.0f), 88.0f);
+    const float r0 = yv_expf_core(xc);
+    return !(x >= -86.0f) ? 0.0f : (x > 88.0f ? __builtin_huge_valf() : r0);
 }
 
 // Value of lane (l + o) % 16 of this lane's 16-lane row (DPP row_ror, a VALU move instead of
@@ -104,36 +106,41 @@ __device__ __forceinline__ void topk_token(LogitFn logit, const float* __restric
 #pragma unroll
     for (int i = 0; i < NV; ++i) z[i] = z[i] / part;
 
-    // top-k by (p desc, index asc)
-    unsigned taken = 0u;
+    // top-k by (p desc, index asc). Each candidate is one 64-bit key, the probability's bits
+    // high (non-negative floats order like their bits) and the inverted expert index low (the
+    // lower index wins a tie), so an argmax step is one unsigned compare and two selects
+    // instead of the short-circuit float-and-index test, whose branches cost more than the
+    // arithmetic. Taken, out-of-range and NaN entries hold key 0, below every candidate (a
+    // NaN probability was never better than anything, so it was never chosen either).
+    unsigned long long key[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int e = l + kLanes * i;
+        key[i] = (e < E && z[i] == z[i])
+                     ? ((unsigned long long)__float_as_uint(z[i]) << 32) | (unsigned)(~e)
+                     : 0ull;
+    }
     float e0 = 0.0f, ts0 = 0.0f, tot = 0.0f;
     my_ts = 0.0f;
     my_id = 0;
     for (int j = 0; j < k; ++j) {
-        float bv = -1.0f;
-        int be = 0x7fffffff;
-        int bi = -1;
+        unsigned long long b = key[0];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int e = l + kLanes * i;
-            if (e < E && !((taken >> i) & 1u) && better(z[i], e, bv, be)) {
-                bv = z[i];
-                be = e;
-                bi = i;
-            }
-        }
-#define YV_ARGSTEP(O)                         \
-    do {                                      \
-        const float ov = rot16<O>(bv);        \
-        const int oe = rot16<O>(be);          \
-        if (better(ov, oe, bv, be)) {         \
-            bv = ov;                          \
-            be = oe;                          \
-        }                                     \
+        for (int i = 1; i < NV; ++i) b = key[i] > b ? key[i] : b;
+#define YV_KEYSTEP(O)                                                                           \
+    do {                                                                                        \
+        const unsigned lo = (unsigned)rot16<O>((int)(unsigned)b);                               \
+        const unsigned hi = (unsigned)rot16<O>((int)(unsigned)(b >> 32));                       \
+        const unsigned long long o = ((unsigned long long)hi << 32) | lo;                       \
+        b = o > b ? o : b;                                                                      \
     } while (0)
-        YV_BFLY16(YV_ARGSTEP);
-#undef YV_ARGSTEP
-        if ((be % kLanes) == l && bi >= 0 && (l + kLanes * bi) == be) taken |= 1u << bi;
+        YV_BFLY16(YV_KEYSTEP);
+#undef YV_KEYSTEP
+        // no candidate left (only with NaN probabilities): probability -1, index INT_MAX
+        const float bv = b != 0ull ? __uint_as_float((unsigned)(b >> 32)) : -1.0f;
+        const int be = b != 0ull ? (int)~(unsigned)b : 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) key[i] = key[i] == b ? 0ull : key[i];  // the owner takes it
         if (j == 0) ts0 = bv;
         const float ej = yv_expf(bv - ts0);
         tot = tot + ej;
