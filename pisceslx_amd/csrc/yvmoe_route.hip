@@ -556,19 +556,22 @@ __global__ __launch_bounds__(256) void route_topk_small_kernel(
         else s_pr[c - E] = v;
     }
     __syncthreads();
-    if (tid >= kLanes) return;  // no barrier follows
-    const int l = tid;
-    int my_id;
-    float my_ts, my_w0;
-    topk_token<NV>([&](int e) { return s_lg[e]; }, bias != nullptr ? s_bias : nullptr, l, E, k, my_id,
-                   my_ts, my_w0);
-    if (l < k) {
-        const size_t s = (size_t)t * k + l;
-        idx_out[s] = (int64_t)my_id;
-        topp[s] = my_ts;
-        w0[s] = my_w0;
-    }
-    if (pred != nullptr) {
+    // no barrier follows: the top-k runs on wavefront 0's first 16 lanes and, at the same time,
+    // the predictor on wavefront 1's first 16 lanes (both read only LDS)
+    if (tid < kLanes) {
+        const int l = tid;
+        int my_id;
+        float my_ts, my_w0;
+        topk_token<NV>([&](int e) { return s_lg[e]; }, bias != nullptr ? s_bias : nullptr, l, E, k, my_id,
+                       my_ts, my_w0);
+        if (l < k) {
+            const size_t s = (size_t)t * k + l;
+            idx_out[s] = (int64_t)my_id;
+            topp[s] = my_ts;
+            w0[s] = my_w0;
+        }
+    } else if (pred != nullptr && tid >= 64 && tid < 64 + kLanes) {
+        const int l = tid - 64;
         const float sv = predictor_token([&](int c) { return s_pr[c]; }, pred_terms, s_b1, s_w2, s_b2, l);
         if (l == 0) score[t] = sv;
     }
