@@ -1162,6 +1162,178 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     else run_tile(std::false_type{});
 }
 
+// ------------------------------------------------------------------ bf16, wide dense form
+// Dense fp32-output GEMM over many tiles (the YvMoEGate projection at prefill): out[N][ldo] =
+// x[N][K] · Wᵀ (+ a column bias), W [ncols][K] bf16 in the 16 x 64 block order.
+//
+// One work-group of four wavefronts per 256 x 256 output tile, a 2 x 2 grid of wavefronts
+// that each own 128 rows x 128 columns: 8 x 8 blocks of v_mfma_f32_16x16x32_bf16, 256 fp32
+// accumulators per lane in AGPRs (an MFMA in inline assembly with the accumulator as one tied
+// AGPR operand: the builtin form let the register allocator copy the accumulators between
+// AGPRs on every K step). A wavefront reads 16 activation and 16 weight fragments per 64-wide
+// chunk for 128 MFMAs (256 LDS bytes per MFMA; the 16-wavefront tile reads 640). Chunks move
+// HBM -> LDS by direct loads through a 2-stage ring (2 x 64 KB), the same swizzled activation
+// rows and as-stored weight blocks as the 16-wavefront tile. The MFMAs of each chunk run in two
+// halves (k = 16 g + 0..7, then 16 g + 8..15, g = lane / 16): the next half's fragment reads
+// and, in the second half, the direct loads of chunk c + 2 are spread among them; between the
+// halves one barrier frees chunk c's stage and publishes chunk c + 1.
+//
+// Weights are the MFMA's first operand: a lane's accumulator then holds 4 consecutive output
+// columns of one row, stored as one 16-byte non-temporal store (the outputs are read once, by
+// another kernel). Measured on the YvMoEGate projection (16,721 x 16,896 x 4,096): the
+// element-wise stores of the activations-first order took a quarter of each tile's time, with
+// every work-group's epilogue at once; this form runs 7-12 % faster than the 16-wavefront tile.
+// Each output accumulates in the 16-wavefront tile's order (chunk by chunk, the k = 16 g + 0..7
+// MFMA before the 16 g + 8..15 one), so the results are bit-identical to it.
+constexpr int WIDE_K = 64;
+__device__ __forceinline__ void dma16s(const void* base, unsigned off, unsigned m0) {
+    asm volatile("global_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "{m0}"(m0) : "memory");
+}
+__device__ __forceinline__ void mfma_acc(f32x4& acc, const bf16x8& a, const bf16x8& b) {
+    asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// s_waitcnt immediate that waits for lgkmcnt <= n only (vmcnt and expcnt at their maxima)
+constexpr int lgkm_only(int n) { return 0xf | (0x3 << 14) | (0x7 << 4) | ((n & 0xf) << 8); }
+
+__global__ __launch_bounds__(256) void gemm_wide_kernel(GemmParams p, int ncb) {
+    constexpr int MBW = 8, NBW = 8;          // 16-row / 16-column blocks per wavefront
+    constexpr int T = MBW * NBW, R = MBW + NBW;  // MFMAs and fragment reads per half chunk
+    constexpr int A_BYTES = TBM * WIDE_K * 2, B_BYTES = TBN * WIDE_K * 2;
+    constexpr int DA = A_BYTES / 1024 / 4, DB = B_BYTES / 1024 / 4;  // 1 KB loads per wavefront
+    __shared__ __attribute__((aligned(1024))) unsigned char lds_a[2][A_BYTES];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds_b[2][B_BYTES];
+    const int lane = threadIdx.x & 63;
+    // uniform in the wavefront (readfirstlane): the direct loads take their base from SGPRs
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wr = wave >> 1, wc = wave & 1;  // 128-row half, 128-column half
+    // items (row tile, column block), column block fastest, in 8 contiguous ranges (one per XCD)
+    const int ntl = (p.nrows + TBM - 1) / TBM;
+    const int total = ntl * ncb;
+    const int per_xcd = (total + 7) / 8;
+    const int local = blockIdx.x / 8;
+    if (local >= per_xcd) return;
+    const int item = (blockIdx.x % 8) * per_xcd + local;
+    if (item >= total) return;
+    const int row0 = (item / ncb) * TBM;
+    const int n0 = (item % ncb) * TBN;
+    const int nks = p.K / WIDE_K;
+
+    // activation block j of this wavefront: tile rows 8 (DA w + j) .. + 7, lane L row + L / 8,
+    // logical chunk (L % 8) ^ (L / 8) ^ (block & 1) (the 16-wavefront tile's swizzle); rows
+    // past the batch re-read row 0 of the tile (their results are not stored). 32-bit byte
+    // offsets from x (the host checks N * lda * 2 < 2^31).
+    unsigned a_off[DA];
+#pragma unroll
+    for (int j = 0; j < DA; ++j) {
+        const int blk = wave * DA + j;
+        const int r = blk * 8 + lane / 8;
+        const int lc = (lane % 8) ^ (lane / 8) ^ (blk & 1);
+        const int gr = (row0 + r < p.nrows) ? row0 + r : row0;
+        a_off[j] = (unsigned)((gr * p.lda + lc * 8) * 2);
+    }
+    // weight 1 KB pieces: piece j = half (j & 1) of the 2 KB block of tile columns
+    // 16 (DB w + j) / 2 .. + 15, landing at (DB w + j) KB; the block's base is uniform
+    const long long b_rowblk = (long long)(p.K / 64) * 2048;  // bytes between 16-column blocks
+    const char* b_base = (const char*)p.B0 + ((n0 >> 4) + wave * (DB / 2)) * b_rowblk;
+    const unsigned b_off = (unsigned)lane * 16;
+    const unsigned a_lds = (unsigned)(size_t)(lds_ptr_t)&lds_a[0][0] + wave * DA * 1024;
+    const unsigned b_lds = (unsigned)(size_t)(lds_ptr_t)&lds_b[0][0] + wave * DB * 1024;
+    auto dma = [&](int c, int st, int j) {  // direct load j (activation pieces first) of chunk c
+        if (j < DA) {
+            dma16s((const char*)p.A + (size_t)c * WIDE_K * 2, a_off[j], a_lds + st * A_BYTES + j * 1024);
+        } else {
+            const int jb = j - DA;
+            dma16s(b_base + (size_t)c * 2048 + (jb >> 1) * b_rowblk + (jb & 1) * 1024, b_off,
+                   b_lds + st * B_BYTES + jb * 1024);
+        }
+    };
+    // fragment reads (k group g = lane / 16): activation rows wr 128 + 16 mb + lane % 16, weight
+    // rows (output columns) 16 (wc NBW + nb) + lane % 16
+    const int g = lane >> 4;
+    const int a_rd0 = swz_a(wr * 128 + (lane & 15), 2 * g);
+    const int a_rd1 = swz_a(wr * 128 + (lane & 15), 2 * g + 1);
+    const int b_rd0 = (wc * NBW) * 2048 + (16 * g + (lane & 15)) * 16;
+
+    f32x4 acc[MBW][NBW];
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NBW; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    bf16x8 fa[2][MBW], fb[2][NBW];  // fragments of the two halves
+    auto read_frag = [&](int st, int h, int q) {  // weight fragments first, then activations
+        if (q < NBW) fb[h][q] = *(const bf16x8*)(&lds_b[st][0] + b_rd0 + q * 2048 + h * 1024);
+        else fa[h][q - NBW] = *(const bf16x8*)(&lds_a[st][0] + (h ? a_rd1 : a_rd0) + (q - NBW) * 16 * 128);
+    };
+#pragma unroll
+    for (int j = 0; j < DA + DB; ++j) dma(0, 0, j);
+#pragma unroll
+    for (int j = 0; j < DA + DB; ++j) dma(min(1, nks - 1), 1, j);
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(DA + DB));  // chunk 0's loads
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int q = 0; q < R; ++q) read_frag(0, 0, q);
+    for (int c = 0; c < nks; ++c) {
+        const int st = c & 1;
+        // half 0 of chunk c; half 1's fragments of chunk c go out meanwhile. MFMA i takes
+        // weight block i / 8 and activation block i % 8, so 8 in a row share their first operand.
+#pragma unroll
+        for (int i = 0; i < T; ++i) {
+            mfma_acc(acc[i % MBW][i / MBW], fb[0][i / MBW], fa[0][i % MBW]);
+#pragma unroll
+            for (int q = (i * R) / T; q < ((i + 1) * R) / T; ++q) read_frag(st, 1, q);
+        }
+        // every wavefront has read chunk c (its LDS reads done) and holds its loads of chunk
+        // c + 1: the barrier frees stage st for chunk c + 2 and publishes chunk c + 1
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+        __builtin_amdgcn_s_waitcnt(lgkm_only(0));  // the builtin: the compiler's count knows it
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        // half 1 of chunk c; half 0's fragments of chunk c + 1 and the direct loads of chunk
+        // c + 2 go out meanwhile (past the last chunk the reads see the idle stage and are not
+        // used, and the loads repeat the last chunk)
+        const int cn = min(c + 2, nks - 1);
+#pragma unroll
+        for (int i = 0; i < T; ++i) {
+            mfma_acc(acc[i % MBW][i / MBW], fb[1][i / MBW], fa[1][i % MBW]);
+#pragma unroll
+            for (int q = (i * R) / T; q < ((i + 1) * R) / T; ++q) read_frag(st ^ 1, 0, q);
+#pragma unroll
+            for (int j = (i * (DA + DB)) / T; j < ((i + 1) * (DA + DB)) / T; ++j) dma(cn, st, j);
+        }
+    }
+    // the repeated loads of the last iterations land before the work-group ends; wait states
+    // between the last MFMAs and the reads of their accumulators
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    // epilogue: the accumulator of block (mb, nb) holds row 16 mb + lane % 16 and the 4
+    // consecutive columns 16 nb + 4 g .. + 3
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) {
+        const int n = n0 + (wc * NBW + nb) * 16 + 4 * g;
+        f32x4 bias = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (p.col_bias != nullptr) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (n + i < p.col_bias_n) bias[i] = p.col_bias[n + i];
+        }
+#pragma unroll
+        for (int mb = 0; mb < MBW; ++mb) {
+            const int r = row0 + wr * 128 + mb * 16 + (lane & 15);
+            if (r < p.nrows) {
+                f32x4 v = acc[mb][nb];
+                if (p.col_bias != nullptr) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (n + i < p.col_bias_n) v[i] = v[i] + bias[i];
+                }
+                __builtin_nontemporal_store(v, (f32x4*)((float*)p.out + (long long)r * p.ldo + n));
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ fp32 activations
 // fp32 activations and fp32 weights (the reference's fp32 configuration).
 template <int EPI, int NCB>
@@ -1520,7 +1692,12 @@ int tile_launch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, con
         return YVMOE_ERR_UNSUPPORTED;
     }
     if constexpr (EPI == EPI_F32) {
-        gemm_tile_kernel<YVMOE_W_BF16, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb);
+        // a grid that fills the chip (and whose activation offsets fit 31 bits) takes the wide
+        // four-wavefront form; fewer tiles (the router GEMM) keep 16 wavefronts per CU
+        if (ntiles_max * ncb >= 256 && (long long)p.nrows * p.lda * 2 < (1ll << 31) && p.kchunk == p.K)
+            gemm_wide_kernel<<<(unsigned)blocks, 256, 0, st>>>(p, ncb);
+        else
+            gemm_tile_kernel<YVMOE_W_BF16, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb);
     } else {
         switch (wf) {
             case YVMOE_W_BF16: gemm_tile_kernel<YVMOE_W_BF16, EPI, 8192, FOLD><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
