@@ -626,6 +626,15 @@ __device__ __forceinline__ float4 dg_load(const GateArgs& a, const float* row, i
     }
     return v;
 }
+// The same with non-temporal loads (a row that is read once).
+template <int NS>
+__device__ __forceinline__ float4 dg_load_nt(const GateArgs& a, const float* row, int i4) {
+    typedef float f32x4v __attribute__((ext_vector_type(4)));
+    f32x4v v = __builtin_nontemporal_load((const f32x4v*)(row + 4 * i4));
+#pragma unroll
+    for (int z = 1; z < NS; ++z) v += __builtin_nontemporal_load((const f32x4v*)(row + z * a.sstride + 4 * i4));
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
 __device__ __forceinline__ unsigned relu_bits(float v) { return v > 0.f ? __float_as_uint(v) : 0u; }
 
 // Lanes below this one with the flag set in the wavefront mask b.
@@ -750,7 +759,7 @@ __global__ __launch_bounds__(64 * kWaveTok) void moegate_wave_kernel(GateArgs a)
                 float4 v[BATCH];
 #pragma unroll
                 for (int b = 0; b < BATCH; ++b)
-                    if (j0 + b < nj) v[b] = dg_load<NS>(a, drow, (j0 + b) * 64 + lane);
+                    if (j0 + b < nj) v[b] = dg_load_nt<NS>(a, drow, (j0 + b) * 64 + lane);
 #pragma unroll
                 for (int b = 0; b < BATCH; ++b) {
                     if (j0 + b >= nj) continue;
