@@ -188,6 +188,9 @@ def test_path_moe_stage_cache(cuda):
 @pytest.mark.parametrize("B,S,H,E,k,scale", [
     (4, 300, 1024, 64, 6, False),
     (2, 520, 2048, 32, 4, True),
+    # hidden 4096, 64 experts: a 16,896-column projection over 5 row tiles of 256 (the last
+    # holding 16 rows), 330 tiles, so the projection takes the wide four-wavefront form
+    (1, 1040, 4096, 64, 6, False),
 ])
 def test_moegate_wave_form_matches_oracle(cuda, oracle, B, S, H, E, k, scale):
     g = _gate(H, E, k, scale_heads=scale, seed=H + E + 1)
