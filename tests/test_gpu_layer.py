@@ -75,6 +75,8 @@ def _run_and_check(oracle, w, skip=None, tokens=None, label=None):
     ("cfg4", {"n_tokens": 384}),
     ("cfg5", {"n_tokens": 384, "num_experts": 32}),
     ("cfg5", {"n_tokens": 64, "num_experts": 32}),       # fp8 weights on the streaming form
+    ("cfg2", {"n_tokens": 1}),                             # one token: six one-row experts
+    ("cfg2", {"n_tokens": 200}),                           # the small-batch routing at 200 tokens
 ])
 def test_layer_matches_oracle(cuda, oracle, name, kw):
     w = make_workload(name, device="cuda", **kw)
