@@ -32,7 +32,7 @@ and prefill token counts, HBM roofline of the kernel.
 routing): layer step and grouped FFN, the FFN against both rooflines.
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
-       python bench.py --pmc-probe {cfg2,cfg3}   (launches only, for counter runs)
+       python bench.py --pmc-probe {cfg2,cfg3,moegate}   (launches only, for counter runs)
 """
 import argparse
 import dataclasses
@@ -66,8 +66,9 @@ def parse():
     ap.add_argument("--no-norm", action="store_true", help="skip the MoE input RMSNorm timing")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip cfg1 / cfg4 / cfg5 (layer step and FFN against both rooflines)")
-    ap.add_argument("--pmc-probe", choices=["cfg2", "cfg3"], default=None,
-                    help="run the calibration copy and 5 expert-FFN launches, nothing timed")
+    ap.add_argument("--pmc-probe", choices=["cfg2", "cfg3", "moegate"], default=None,
+                    help="run the calibration copy and 5 expert-FFN launches (moegate: 3 YvMoEGate "
+                         "prefill gate calls), nothing timed")
     return ap.parse_args()
 
 
@@ -84,6 +85,25 @@ def pmc_probe(name):
         torch.bitwise_not(src, out=dst)
     torch.cuda.synchronize()
     del src, dst
+    if name == "moegate":  # the prefill gate call of bench's "moegate" object
+        import dataclasses
+        from pisceslx_amd import _lib
+        from pisceslx_amd.gate import YvMoEGate
+        from pisceslx_amd.workloads import seq_lengths
+        spec = make_workload("cfg2", device="cuda", seed=0).spec
+        N = sum(seq_lengths("cfg3", 0))
+        torch.manual_seed(0)
+        g = YvMoEGate(spec.hidden, spec.num_experts, top_k=spec.top_k, device="cuda",
+                      dtype=torch.bfloat16).eval()
+        x = torch.randn(N, spec.hidden, device="cuda",
+                        generator=torch.Generator(device="cuda").manual_seed(3)).to(torch.bfloat16)
+        st0 = g.gate_state(_lib.ACT_BF16, N)
+        ws = torch.empty(1 << 31, dtype=torch.uint8, device="cuda")
+        for _ in range(3):
+            yvf.moegate_forward(x, st0, spec.top_k, workspace=ws)
+        torch.cuda.synchronize()
+        print(f"pmc probe {name}: done", flush=True)
+        return
     w = make_workload(name, device="cuda", seed=0)
     st = router_state(w)
     ws = torch.empty(yvf.workspace_bytes(w.n_tokens, 1, st, w.experts), dtype=torch.uint8, device="cuda")
