@@ -600,7 +600,8 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
 // holds, in index order, every entry seen so far that can still be among the sel_k largest,
 // and a threshold thr admits only entries above it:
 //   - an entry is appended when its relu'd bit pattern exceeds thr (non-negative floats order
-//     like their bits; thr starts at 0, so the first entries admitted are the positive ones);
+//     like their bits; thr starts at 0, so the first entries admitted are the positive ones;
+//     the test is one signed integer compare of the raw bits);
 //   - when the buffer would overflow it is compacted to exactly the sel_k largest so far (the
 //     entries above T, the sel_k-th largest bit pattern found by bisection, and the
 //     lowest-index entries equal to T), and thr becomes T: a later entry equal to T ranks
@@ -635,16 +636,17 @@ __device__ __forceinline__ float4 dg_load_nt(const GateArgs& a, const float* row
     for (int z = 1; z < NS; ++z) v += __builtin_nontemporal_load((const f32x4v*)(row + z * a.sstride + 4 * i4));
     return make_float4(v[0], v[1], v[2], v[3]);
 }
-__device__ __forceinline__ unsigned relu_bits(float v) { return v > 0.f ? __float_as_uint(v) : 0u; }
 
 // Lanes below this one with the flag set in the wavefront mask b.
 __device__ __forceinline__ int lanes_below(unsigned long long b) {
     return (int)__builtin_amdgcn_mbcnt_hi((unsigned)(b >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)b, 0u));
 }
-// Compacts the wavefront's candidate buffer (K <= n <= kWaveCand entries in index order, relu'd
-// bit patterns in cu) to its K largest (ties to the lower index), in index order; returns T,
-// the K-th largest bit pattern. The bisection for T runs on the entries held in registers.
-__device__ unsigned wave_compact(unsigned* cu, int* ci, int n, int K) {
+// Compacts the wavefront's candidate buffer (K <= n <= kWaveCand entries in index order, bit
+// patterns of positive floats in cu, none below lo0) to its K largest (ties to the lower
+// index), in index order; returns T, the K-th largest bit pattern. The bisection for T runs on
+// the entries held in registers and counts with wavefront ballots (one compare per register and
+// step; the population counts are scalar work).
+__device__ unsigned wave_compact(unsigned* cu, int* ci, int n, int K, unsigned lo0) {
     constexpr int PER = kWaveCand / 64;
     const int lane = threadIdx.x & 63;
     unsigned r[PER];
@@ -660,10 +662,10 @@ __device__ unsigned wave_compact(unsigned* cu, int* ci, int n, int K) {
     auto cnt_ge = [&](unsigned x) {
         unsigned c = 0u;
 #pragma unroll
-        for (int m = 0; m < PER; ++m) c += r[m] >= x ? 1u : 0u;
-        return (unsigned)wave_sum((float)c);  // counts <= kWaveCand: exact in fp32
+        for (int m = 0; m < PER; ++m) c += (unsigned)__popcll(__ballot(r[m] >= x));
+        return c;
     };
-    unsigned lo = 1u, hi = mx + 1u;  // cnt(lo) = n >= K, cnt(hi) = 0 < K
+    unsigned lo = lo0, hi = mx + 1u;  // cnt(lo) = n >= K, cnt(hi) = 0 < K
     while (hi - lo > 1u) {
         const unsigned mid = lo + (hi - lo) / 2u;
         if (cnt_ge(mid) >= (unsigned)K) lo = mid;
@@ -763,22 +765,26 @@ __global__ __launch_bounds__(64 * kWaveTok) void moegate_wave_kernel(GateArgs a)
 #pragma unroll
                 for (int b = 0; b < BATCH; ++b) {
                     if (j0 + b >= nj) continue;
-                    const unsigned u[4] = {relu_bits(v[b].x), relu_bits(v[b].y), relu_bits(v[b].z), relu_bits(v[b].w)};
+                    // relu'd value above thr <=> the bit pattern, as a signed integer, above thr
+                    // (thr < 2^31; negative values and zeros are at most 0 as integers; a NaN
+                    // with the sign bit clear counts as the largest, as torch.topk ranks NaN)
+                    const int u[4] = {__float_as_int(v[b].x), __float_as_int(v[b].y), __float_as_int(v[b].z),
+                                      __float_as_int(v[b].w)};
                     unsigned long long bl[4];
                     int tot = 0;
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        bl[c] = __ballot(u[c] > thr);
+                        bl[c] = __ballot(u[c] > (int)thr);
                         tot += __popcll(bl[c]);
                     }
                     if (tot == 0) continue;  // wave-uniform
                     if (n + tot > kWaveCand) {
-                        thr = wave_compact(c_bits[wave], c_idx[wave], n, K);
+                        thr = wave_compact(c_bits[wave], c_idx[wave], n, K, thr);
                         n = K;
                         tot = 0;
 #pragma unroll
                         for (int c = 0; c < 4; ++c) {
-                            bl[c] = __ballot(u[c] > thr);
+                            bl[c] = __ballot(u[c] > (int)thr);
                             tot += __popcll(bl[c]);
                         }
                     }
@@ -787,8 +793,8 @@ __global__ __launch_bounds__(64 * kWaveTok) void moegate_wave_kernel(GateArgs a)
                               lanes_below(bl[3]);
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        if (u[c] > thr) {
-                            c_bits[wave][pos] = u[c];
+                        if (u[c] > (int)thr) {
+                            c_bits[wave][pos] = (unsigned)u[c];
                             c_idx[wave][pos] = 4 * ((j0 + b) * 64 + lane) + c;
                             ++pos;
                         }
@@ -797,7 +803,7 @@ __global__ __launch_bounds__(64 * kWaveTok) void moegate_wave_kernel(GateArgs a)
                 }
             }
             if (n > K) {
-                wave_compact(c_bits[wave], c_idx[wave], n, K);
+                wave_compact(c_bits[wave], c_idx[wave], n, K, thr);
                 n = K;
             }
             const int C = n;
@@ -838,15 +844,19 @@ __global__ __launch_bounds__(64 * kWaveTok) void moegate_wave_kernel(GateArgs a)
         // ------------------------------------------------------------ SoftMoE, logits, loss
         float soft = 0.f, soft_tot = 0.f;
         if (a.mask & YVMOE_HEAD_SOFT) {
-            // torch.median: the lower middle value (rank, ties by index)
-            const int lkb = __float_as_int(lk);
-            unsigned rr = 0u;
-            for (int j = 0; j < E; ++j) {
-                const float xj = __int_as_float(__builtin_amdgcn_readlane(lkb, j));
-                rr += (xj < lk || (xj == lk && j < lane)) ? 1u : 0u;
+            // torch.median: the lower middle value, the smallest value with more than (E - 1) / 2
+            // of the E values at or below it; bisection over order-preserving integer keys of
+            // the floats, counted by wavefront ballots
+            const unsigned lkb = __float_as_uint(lk);
+            const unsigned key = lkb ^ ((lkb >> 31) ? 0xffffffffu : 0x80000000u);
+            const unsigned need = (unsigned)((E - 1) / 2) + 1u;
+            unsigned lo = 0u, hi = 0xffffffffu;
+            while (lo < hi) {
+                const unsigned mid = lo + (hi - lo) / 2u;
+                if ((unsigned)__popcll(__ballot(is_e && key <= mid)) >= need) hi = mid;
+                else lo = mid + 1u;
             }
-            const int ml = __ffsll((long long)__ballot(is_e && rr == (unsigned)((E - 1) / 2))) - 1;
-            const float med = __shfl(lk, ml);
+            const float med = __uint_as_float(lo ^ ((lo >> 31) ? 0x80000000u : 0xffffffffu));
             const float mx = wave_max(is_e ? lv : -INFINITY);
             const float ex = is_e ? expf(lv - mx) : 0.f;
             const float se = wave_sum(ex);
