@@ -42,6 +42,12 @@
 #ifndef YV_U1
 #define YV_U1 4  // k-steps per staged chunk, streaming gate/up
 #endif
+#ifndef YV_PF1
+#define YV_PF1 false  // streaming gate/up: weights one chunk ahead (false measured best)
+#endif
+#ifndef YV_PF2
+#define YV_PF2 false  // streaming down projection: weights one chunk ahead (false measured best)
+#endif
 #ifndef YV_U2
 #define YV_U2 4  // k-steps per staged chunk, streaming down projection
 #endif
@@ -1948,7 +1954,7 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.kchunk = H;
     const bool streaming = (maxrb == 1);
     int rc = tiled ? tile_dispatch<EPI_SWIGLU>(wf, p, T, st, "expert_gemm1", tt.fold > 0)
-           : streaming ? stream_dispatch<EPI_SWIGLU, YV_U1, YV_NB1>(wf, p, T, st, "expert_gemm1")
+           : streaming ? stream_dispatch<EPI_SWIGLU, YV_U1, YV_NB1, 1, YV_PF1>(wf, p, T, st, "expert_gemm1")
                        : gemm_dispatch<EPI_SWIGLU>(act, wf, p, T, (F % 32 == 0) ? 2 : 1, 1, st,
                                                    "expert_gemm1", maxrb);
     if (rc != YVMOE_OK) return rc;
@@ -1970,7 +1976,7 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.ldo = H;
     p.kchunk = F;
     if (tiled) return tile_dispatch<EPI_DOWN>(wf, p, T, st, "expert_gemm2", tt.fold > 0);
-    return streaming ? stream_dispatch<EPI_DOWN, YV_U2, YV_NB2>(wf, p, T, st, "expert_gemm2")
+    return streaming ? stream_dispatch<EPI_DOWN, YV_U2, YV_NB2, 1, YV_PF2>(wf, p, T, st, "expert_gemm2")
                      : gemm_dispatch<EPI_DOWN>(act, wf, p, T, (H % 32 == 0) ? 2 : 1, 1, st,
                                                "expert_gemm2", maxrb);
 }
