@@ -610,6 +610,8 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
 //     fewer), ranked in (value descending, index ascending) order.
 constexpr int kWaveTok = 4;     // wavefronts (tokens in flight) per work-group
 constexpr int kWaveCand = 512;  // candidate buffer per wavefront (compaction leaves <= 64)
+// a compaction leaves at most kGateMaxSel entries, and one row load adds at most 256
+static_assert(kWaveCand % 64 == 0 && kWaveCand >= kGateMaxSel + 256, "candidate buffer too small");
 // Below this many tokens a wavefront per token cannot stream the rows fast enough (decode, 64
 // tokens: 110 us against 71 us for a work-group per token); the work-group form runs instead.
 constexpr int kWaveMinTokens = 1024;
