@@ -45,6 +45,12 @@
 #ifndef YV_PF1
 #define YV_PF1 false  // streaming gate/up: weights one chunk ahead (false measured best)
 #endif
+#ifndef YV_WV1
+#define YV_WV1 4  // wavefronts per work-group, streaming gate/up (4 measured best)
+#endif
+#ifndef YV_WV2
+#define YV_WV2 4  // wavefronts per work-group, streaming down projection (4 measured best)
+#endif
 #ifndef YV_PF2
 #define YV_PF2 false  // streaming down projection: weights one chunk ahead (false measured best)
 #endif
@@ -478,7 +484,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(GemmParams p) {
 // that measured closest to the HBM ceiling), reading activation fragments from LDS. More
 // column blocks per wavefront put more weight bytes in flight per activation chunk and per
 // barrier.
-template <int WF, int EPI, int U, int MAXRB, int NB, bool PF = false>
+template <int WF, int EPI, int U, int MAXRB, int NB, bool PF = false, int WV = 4>
 __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int cgroup, int kz,
                                             uint4 (&As)[2][16 * MAXRB * (U * 8 + 1)]) {
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
@@ -486,8 +492,10 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
     constexpr int ROWS = 16 * MAXRB;
     constexpr int ROW_U4 = U * 8 + 1;            // uint4 per staged row (U*64 bf16 + pad)
     constexpr int CHUNK_U4 = ROWS * U * 8;       // uint4 of one chunk
-    constexpr int PER_THREAD = CHUNK_U4 / 256;   // uint4 each thread stages per chunk
-    static_assert(CHUNK_U4 % 256 == 0, "chunk must split evenly over 256 threads");
+    constexpr int NT = 64 * WV;                  // threads of the work-group (WV wavefronts)
+    constexpr int PER_THREAD = CHUNK_U4 / NT;    // uint4 each thread stages per chunk
+    static_assert(CHUNK_U4 % NT == 0, "chunk must split evenly over the work-group");
+    static_assert(WV == 2 || WV == 4, "two or four wavefronts per work-group");
     static_assert(2 * ROWS * ROW_U4 * 16 >= 2 * 64 * MAXRB * NB * 16, "LDS too small for the swap");
     typedef BLoad<WF> BL;
     const int tid = threadIdx.x;
@@ -502,20 +510,20 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
     const int nrb = (nvalid + 15) / 16;
     const int mat = SWIGLU ? (wave & 1) : 0;  // 0: gate (or down), 1: up
     // first column of block b of this wavefront
-    const int colw = SWIGLU ? (cgroup * 2 + (wave >> 1)) * 16 * NB : (cgroup * 4 + wave) * 16 * NB;
+    const int colw = SWIGLU ? (cgroup * (WV / 2) + (wave >> 1)) * 16 * NB : (cgroup * WV + wave) * 16 * NB;
     // K range of split kz (EPI_F32 writes split kz's partial sums at kz * split_stride)
     const int kbeg = kz * p.kchunk;
     const int kend = min(p.K, kbeg + p.kchunk);
     const int nks = (kend - kbeg) / 64;
     const int nchunks = (nks + U - 1) / U;
 
-    // staging: thread t copies uint4 q = t + j*256 of each chunk: row q / (U*8), column q % (U*8)
+    // staging: thread t copies uint4 q = t + j*NT of each chunk: row q / (U*8), column q % (U*8)
     const char* srow[PER_THREAD];
     int sdst[PER_THREAD], scol[PER_THREAD];
     bool sval[PER_THREAD];
 #pragma unroll
     for (int j = 0; j < PER_THREAD; ++j) {
-        const int q = tid + j * 256;
+        const int q = tid + j * NT;
         const int r = q / (U * 8);
         scol[j] = q % (U * 8);
         sval[j] = r < nvalid;
@@ -752,8 +760,8 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
 // contiguous ranges, one per XCD: the tiles that share weights (the 16-row tiles of a shared
 // expert, which all read the same columns) then run together on one XCD and fetch those
 // weights from HBM once into its L2 instead of once per tile.
-template <int WF, int EPI, int U, int MAXRB, int NB, bool PF = false>
-__global__ __launch_bounds__(256) void gemm_stream_kernel(GemmParams p, int ngroups, int nsplit) {
+template <int WF, int EPI, int U, int MAXRB, int NB, bool PF = false, int WV = 4>
+__global__ __launch_bounds__(64 * WV) void gemm_stream_kernel(GemmParams p, int ngroups, int nsplit) {
     __shared__ uint4 As[2][16 * MAXRB * (U * 8 + 1)];
     const int nt = p.tile_seg == nullptr ? (p.nrows + 16 * MAXRB - 1) / (16 * MAXRB) : *p.ntiles;
     const int nitems = nt * ngroups * nsplit;
@@ -763,7 +771,7 @@ __global__ __launch_bounds__(256) void gemm_stream_kernel(GemmParams p, int ngro
     const int item = (blockIdx.x % 8) * per_xcd + local;
     if (item >= nitems) return;
     const int rest = item / nt;  // tile fastest, then column group, then K split
-    stream_item<WF, EPI, U, MAXRB, NB, PF>(p, item % nt, rest % ngroups, rest / ngroups, As);
+    stream_item<WF, EPI, U, MAXRB, NB, PF, WV>(p, item % nt, rest % ngroups, rest / ngroups, As);
 }
 
 // ------------------------------------------------------------------ bf16, LDS-tiled form
@@ -1640,13 +1648,13 @@ __global__ __launch_bounds__(256) void reduce_splits_kernel(const float* __restr
 
 // Streaming (decode) form: one (tile, column group) item per work-group; NB 16-column
 // blocks per wavefront.
-template <int EPI, int U, int NB, int MAXRB = 1, bool PF = false>
+template <int EPI, int U, int NB, int MAXRB = 1, bool PF = false, int WV = 4>
 int stream_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, const char* name,
                     int nsplit = 1) {
-    const int ngroups = (EPI == EPI_SWIGLU) ? ceil_div(p.ncols, 32 * NB) : ceil_div(p.ncols, 64 * NB);
+    const int ngroups = (EPI == EPI_SWIGLU) ? ceil_div(p.ncols, 8 * WV * NB) : ceil_div(p.ncols, 16 * WV * NB);
     const long long items = 8LL * ceil_div(ntiles_max * ngroups * nsplit, 8);
     if (items <= 0) return YVMOE_OK;
-#define YV_ST(WFV) gemm_stream_kernel<WFV, EPI, U, MAXRB, NB, PF><<<(unsigned)items, 256, 0, st>>>(p, ngroups, nsplit)
+#define YV_ST(WFV) gemm_stream_kernel<WFV, EPI, U, MAXRB, NB, PF, WV><<<(unsigned)items, 64 * WV, 0, st>>>(p, ngroups, nsplit)
     if constexpr (EPI == EPI_F32) {  // dense fp32 output: bf16 weights only
         if (wf != YVMOE_W_BF16) {
             set_error("%s: fp32-output streaming form needs bf16 weights", name);
@@ -1954,7 +1962,7 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.kchunk = H;
     const bool streaming = (maxrb == 1);
     int rc = tiled ? tile_dispatch<EPI_SWIGLU>(wf, p, T, st, "expert_gemm1", tt.fold > 0)
-           : streaming ? stream_dispatch<EPI_SWIGLU, YV_U1, YV_NB1, 1, YV_PF1>(wf, p, T, st, "expert_gemm1")
+           : streaming ? stream_dispatch<EPI_SWIGLU, YV_U1, YV_NB1, 1, YV_PF1, YV_WV1>(wf, p, T, st, "expert_gemm1")
                        : gemm_dispatch<EPI_SWIGLU>(act, wf, p, T, (F % 32 == 0) ? 2 : 1, 1, st,
                                                    "expert_gemm1", maxrb);
     if (rc != YVMOE_OK) return rc;
@@ -1976,7 +1984,7 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.ldo = H;
     p.kchunk = F;
     if (tiled) return tile_dispatch<EPI_DOWN>(wf, p, T, st, "expert_gemm2", tt.fold > 0);
-    return streaming ? stream_dispatch<EPI_DOWN, YV_U2, YV_NB2, 1, YV_PF2>(wf, p, T, st, "expert_gemm2")
+    return streaming ? stream_dispatch<EPI_DOWN, YV_U2, YV_NB2, 1, YV_PF2, YV_WV2>(wf, p, T, st, "expert_gemm2")
                      : gemm_dispatch<EPI_DOWN>(act, wf, p, T, (H % 32 == 0) ? 2 : 1, 1, st,
                                                "expert_gemm2", maxrb);
 }
