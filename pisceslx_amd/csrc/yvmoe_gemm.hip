@@ -495,8 +495,8 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
     constexpr int NT = 64 * WV;                  // threads of the work-group (WV wavefronts)
     constexpr int PER_THREAD = CHUNK_U4 / NT;    // uint4 each thread stages per chunk
     static_assert(CHUNK_U4 % NT == 0, "chunk must split evenly over the work-group");
-    static_assert(WV == 2 || WV == 4, "two or four wavefronts per work-group");
-    static_assert(2 * ROWS * ROW_U4 * 16 >= 2 * 64 * MAXRB * NB * 16, "LDS too small for the swap");
+    static_assert(WV == 2 || WV == 4 || WV == 8, "two, four or eight wavefronts per work-group");
+    static_assert(2 * ROWS * ROW_U4 * 16 >= (WV / 2) * 64 * MAXRB * NB * 16, "LDS too small for the swap");
     typedef BLoad<WF> BL;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
