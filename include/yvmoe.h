@@ -250,8 +250,11 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
  * routine). This entry point has no counterpart in the reference; it is for callers that
  * cannot allocate device memory: code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc. The caller still passes x, out, shared_out and the routing buffers.
- * The scratch is one device array of YVMOE_STATIC_SCRATCH_BYTES per GPU, held from the first
- * call on that GPU until the process ends; a call whose yvmoe_workspace_bytes() exceeds it
+ * The scratch is one device array of YVMOE_STATIC_SCRATCH_BYTES per GPU. It is part of the
+ * library's device code, so it is reserved on a GPU when that code is loaded there (at the
+ * latest by the first call of any entry point on that GPU, whether or not this one is ever
+ * called) and held until the process ends: every process that uses the library pays 64 MiB
+ * of device memory per GPU it runs on. A call whose yvmoe_workspace_bytes() exceeds it
  * returns YVMOE_ERR_WORKSPACE (at cfg2's shape, hidden 4096 / 64 experts / top-6 / 2 shared,
  * up to 689 tokens fit). Every call on one GPU shares that GPU's scratch, which keeps the last
  * call's contents: calls that overlap on one GPU (other streams, other host threads) race.

@@ -250,6 +250,10 @@ def load_packed(path: str, device="cuda") -> PackedLayer:
                             int(meta["num_shared"]), int(meta["hidden"]), int(meta["ffn"]),
                             t["experts.w_gate"], t["experts.w_up"], t["experts.w_down"],
                             t.get("experts.s_gate"), t.get("experts.s_up"), t.get("experts.s_down"))
+    if experts.format == FORMAT_BY_NAME["int4"]:
+        from .quant import check_int4_scales
+        for name in ("s_gate", "s_up", "s_down"):
+            check_int4_scales(getattr(experts, name), f"{path}: experts.{name}")
     router = {k[len("router."):]: v for k, v in t.items() if k.startswith("router.")}
     return PackedLayer(experts, router, t.get("shared_expert_weight"), meta)
 

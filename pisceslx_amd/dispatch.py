@@ -18,6 +18,9 @@ Differences a caller can observe, all deliberate:
   reference rounds each weighted product and each ``index_add_`` to the output dtype (on a
   GPU in an unordered atomic sequence), and with fp32 weights and bf16 activations its
   ``index_add_`` raises (source and destination dtypes differ), where this operator computes;
+* the operator is an inference forward: in training mode (the module's or an expert's), or
+  with inputs that require grad while autograd is on, it raises NotImplementedError instead of
+  returning a detached output without the experts' dropout;
 * an index outside ``[0, E)`` is never read through: those slots add nothing, and with
   ``check_indices`` (the default) the forward raises RuntimeError as the reference's bincount
   / module indexing does — that check reads one int from the device; set
@@ -70,6 +73,25 @@ def packed_from_modules(experts: Sequence[nn.Module], dtype: torch.dtype, device
     return packed
 
 
+def _reject_training(module: nn.Module, x_flat: torch.Tensor, routing_weights: torch.Tensor,
+                     experts: ExpertsArg) -> None:
+    """The kernels are an inference forward: no autograd graph and no expert dropout
+    (``YvSwiGLUExpert.forward`` applies dropout in training mode, model/moe/expert.py:484-489).
+    A call that would need either raises instead of returning a detached output."""
+    if module.training:
+        raise NotImplementedError("PiscesLxFusedMoEDispatch on MI355X is an inference operator; "
+                                  "call .eval()")
+    if torch.is_grad_enabled() and (x_flat.requires_grad or routing_weights.requires_grad):
+        raise NotImplementedError("PiscesLxFusedMoEDispatch on MI355X computes no gradients: run "
+                                  "it under torch.no_grad() / inference_mode or pass tensors that "
+                                  "do not require grad")
+    if not isinstance(experts, PackedExperts):
+        for m in experts:
+            if m.training:
+                raise NotImplementedError("expert modules in training mode (dropout active) are "
+                                          "not supported; call .eval() on the experts")
+
+
 class PiscesLxFusedMoEDispatch(nn.Module):
     """Sort-based MoE dispatch (opss/infer/fused_moe.py:32-123) on the MI355X kernels."""
 
@@ -82,6 +104,7 @@ class PiscesLxFusedMoEDispatch(nn.Module):
 
     def forward(self, x_flat: torch.Tensor, routing_weights: torch.Tensor,
                 expert_indices: torch.Tensor, experts: ExpertsArg, collect_stats: bool = False):
+        _reject_training(self, x_flat, routing_weights, experts)
         num_tokens = x_flat.shape[0]
         hidden = x_flat.shape[-1]
         flat_indices = expert_indices.reshape(-1)
@@ -135,5 +158,7 @@ class PiscesLxFusedMoe:
     def fused_moe_dispatch(x_flat: torch.Tensor, routing_weights: torch.Tensor,
                            expert_indices: torch.Tensor, experts: ExpertsArg, num_experts: int,
                            top_k: int) -> torch.Tensor:
-        return PiscesLxFusedMoEDispatch(num_experts, top_k)(x_flat, routing_weights,
-                                                           expert_indices, experts)
+        # a functional call: the operator itself holds no training state (the experts' and the
+        # inputs' are still checked)
+        return PiscesLxFusedMoEDispatch(num_experts, top_k).eval()(x_flat, routing_weights,
+                                                                  expert_indices, experts)

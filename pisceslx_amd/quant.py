@@ -61,6 +61,23 @@ def dequantize_int8(q: torch.Tensor, s: torch.Tensor) -> torch.Tensor:
 
 
 # ------------------------------------------------------------------ int4 g128
+# The kernels' int4 conversion forms (q - 8) * s as (1024 + q) * s - 1032 * s in one fused
+# multiply-add, exact (bit-identical to converting q - 8 and multiplying) for bf16 scales with
+# 2^-126 <= |s| < 2^97 (and s = 0): above that 1032 * s overflows, below it s / 16 loses bits.
+INT4_SCALE_MIN, INT4_SCALE_MAX = 2.0 ** -126, 2.0 ** 97
+
+
+def check_int4_scales(s: torch.Tensor, what: str = "int4 scales") -> None:
+    """Raise ValueError for a bf16 group scale the kernels cannot apply exactly: not finite,
+    |s| >= 2^97, or 0 < |s| < 2^-126 (subnormal)."""
+    a = s.float().abs()
+    bad = ~torch.isfinite(a) | (a >= INT4_SCALE_MAX) | ((a > 0) & (a < INT4_SCALE_MIN))
+    if bool(bad.any()):
+        v = float(s.float().reshape(-1)[bad.reshape(-1)][0])
+        raise ValueError(f"{what}: scale {v!r} outside the supported range 2^-126 <= |s| < 2^97 "
+                         f"(or 0)")
+
+
 def quantize_int4(w: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
     w = w.float()
     out, inn = w.shape
@@ -68,6 +85,7 @@ def quantize_int4(w: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
         raise ValueError(f"int4 group-128 needs in % 128 == 0, got {inn}")
     wg = w.view(out, inn // 128, 128)
     s = (wg.abs().amax(dim=-1) / 7.0).clamp(min=1e-8).to(torch.bfloat16)
+    check_int4_scales(s, "int4 quantization")
     q = (torch.round(wg / s.float()[..., None]) + 8).clamp(0, 15).to(torch.uint8).view(out, inn)
     packed = q[:, 0::2] | (q[:, 1::2] << 4)
     return packed.contiguous(), s

@@ -9,7 +9,7 @@ BF16_MAX_ABS, BF16_COS = 2e-2, 0.9999
 F32_MAX_ABS, F32_COS = 1e-4, 0.999999
 
 # one entry per comparison: (label, elements, max_abs, cosine, elements above the max-abs
-# bound, elements that needed the two-ulp allowance)
+# bound, dtype)
 PARITY_RECORDS = []
 
 
@@ -29,13 +29,25 @@ def bf16_ulp(v: torch.Tensor) -> torch.Tensor:
     return torch.exp2(torch.floor(torch.log2(a)) - 7)
 
 
+def bf16_allowance(want: torch.Tensor) -> torch.Tensor:
+    """Per-element bound of the bf16 layer-output check: 2e-2, widened only where |want| >= 2,
+    to two bf16 steps in [2, 4) (0.03125; the reference's own bf16 chain, torch's F.linear,
+    lands two steps from the correctly rounded value there at cfg4, pinned by
+    tests/test_oracle_bf16_envelope.py) and to one step, i.e. the adjacent bf16 value, from 4 up
+    (the least by which two roundings of nearly the same fp32 sum can differ)."""
+    a = want.double().abs()
+    ulp = bf16_ulp(want)
+    steps = torch.where(a < 4.0, torch.full_like(a, 2.0), torch.ones_like(a))
+    wide = torch.where(a >= 2.0, steps * ulp, torch.zeros_like(a))
+    return torch.maximum(torch.full_like(a, BF16_MAX_ABS), wide)
+
+
 def check_close(got: torch.Tensor, want: torch.Tensor, label: str):
     """Layer-output tolerance. fp32: max-abs <= 1e-4 and cosine >= 0.999999. bf16: cosine >=
-    0.9999 and every element within max(2e-2, two bf16 ulps of the reference value), with at
-    most 1e-5 of the elements beyond 2e-2 (above |out| = 2 one bf16 ulp is 0.0156, 0.031 above
-    4: two correct bf16 chains that differ only in fp32 summation order can differ there by
-    more than 2e-2). Records the comparison for the parity summary; returns (max_abs, cosine,
-    elements above 2e-2)."""
+    0.9999 and every element within ``bf16_allowance`` of the reference value (2e-2; at |want|
+    in [2, 4) two bf16 steps = 0.03125, from 4 up the adjacent bf16 value), with at most 1e-5
+    of the elements beyond 2e-2. Records the comparison for the parity summary; returns
+    (max_abs, cosine, elements above 2e-2)."""
     got, want = got.cpu(), want.cpu()
     if want.dtype == torch.float32:
         tol_abs, tol_cos = F32_MAX_ABS, F32_COS
@@ -43,7 +55,7 @@ def check_close(got: torch.Tensor, want: torch.Tensor, label: str):
         tol_abs, tol_cos = BF16_MAX_ABS, BF16_COS
     d = (got.double() - want.double()).abs()
     if want.dtype == torch.bfloat16:
-        bound = torch.maximum(torch.full_like(d, tol_abs), 2 * bf16_ulp(want))
+        bound = bf16_allowance(want)
     else:
         bound = torch.full_like(d, tol_abs)
     beyond = int((d > bound).sum()) if d.numel() else 0
@@ -53,7 +65,7 @@ def check_close(got: torch.Tensor, want: torch.Tensor, label: str):
     PARITY_RECORDS.append((label, d.numel(), ma, cs, over, str(want.dtype).replace("torch.", "")))
     print(f"parity {label}: max_abs={ma:.3e} cos={cs:.7f} above_{tol_abs:g}={over}/{d.numel()}",
           flush=True)
-    assert beyond == 0, f"{label}: {beyond} elements beyond max({tol_abs}, 2 ulp); max_abs={ma}"
+    assert beyond == 0, f"{label}: {beyond} elements beyond the bf16 allowance; max_abs={ma}"
     assert over <= 1e-5 * d.numel(), f"{label}: {over} elements above {tol_abs}; max_abs={ma}"
     assert cs >= tol_cos, f"{label}: cosine {cs}"
     return ma, cs, over

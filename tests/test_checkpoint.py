@@ -122,6 +122,24 @@ def test_convert_and_load(tmp_path, kind, fmt):
         assert torch.equal(pl.shared_expert_weight, torch.tensor([0.25, 0.75]))
 
 
+def test_load_packed_rejects_int4_scales_out_of_range(tmp_path):
+    from safetensors.torch import load_file, save_file
+    path, _, _ = _checkpoint(tmp_path, "safetensors")
+    dst = str(tmp_path / "l0.safetensors")
+    ck.convert(path, dst, "model.layers.0.mlp.", "int4")
+    ck.load_packed(dst, device="cpu")
+    from safetensors import safe_open
+    with safe_open(dst, framework="pt", device="cpu") as f:
+        meta = dict(f.metadata())
+    t = load_file(dst)
+    t["experts.s_down"] = t["experts.s_down"].clone()
+    t["experts.s_down"].view(-1)[5] = 2.0 ** 100
+    bad = str(tmp_path / "bad.safetensors")
+    save_file(t, bad, metadata=meta)
+    with pytest.raises(ValueError, match="experts.s_down.*outside the supported range"):
+        ck.load_packed(bad, device="cpu")
+
+
 def test_layer_loads_packed_and_checkpoint(tmp_path):
     from pisceslx_amd import YvDeepSeekMoELayer
 

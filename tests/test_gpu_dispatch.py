@@ -79,6 +79,9 @@ def _check_dispatch(oracle, w, idx, wts, label, tokens=None, weight_dtype=torch.
     ("cfg4", {"n_tokens": 96}, 8),
     ("cfg5", {"n_tokens": 200, "num_experts": 32}, 8),
     ("cfg5", {"n_tokens": 64, "num_experts": 32}, 8),   # fp8 weights on the streaming form
+    ("cfg5", {"n_tokens": 200, "num_experts": 32}, 12),  # the combine's second 8-slot chunk
+    ("cfg5", {"n_tokens": 64, "num_experts": 32}, 16),   # the operator's largest k
+    ("cfg2", {"n_tokens": 100}, 1),
 ])
 def test_dispatch_matches_oracle(cuda, oracle, name, kw, k):
     w = make_workload(name, device=cuda, **kw)
@@ -110,12 +113,27 @@ def test_dispatch_duplicates_and_invalid_indices(cuda, oracle):
     wts[4] = 0.0
     out = _check_dispatch(oracle, w, idx, wts, "cfg2 N=40 duplicates / invalid indices")
     assert torch.count_nonzero(out[3]) == 0 and torch.count_nonzero(out[4]) == 0
-    m = PiscesLxFusedMoEDispatch(E, 4)
+    m = PiscesLxFusedMoEDispatch(E, 4).eval()
     with pytest.raises(RuntimeError, match="outside"):
         m(w.x, torch.from_numpy(wts).to(cuda), torch.from_numpy(idx).to(cuda), w.experts)
     m.check_indices = False
     got = m(w.x, torch.from_numpy(wts).to(cuda), torch.from_numpy(idx).to(cuda), w.experts)
     assert torch.equal(got, out)
+
+
+def test_module_one_dimensional_indices(cuda, oracle):
+    """expert_indices of shape [N] (one assignment per token, fused_moe.py:72-76) with routing
+    weights of shape [N], through the module mirror."""
+    w = make_workload("cfg2", device=cuda, n_tokens=90)
+    N, E = 90, w.spec.num_experts
+    idx, wts = _routing(N, 1, E, seed=15)
+    m = PiscesLxFusedMoEDispatch(E, 1).eval()
+    out = m(w.x, torch.from_numpy(wts.reshape(-1)).to(cuda), torch.from_numpy(idx.reshape(-1)).to(cuda),
+            w.experts)
+    torch.cuda.synchronize()
+    assert out.shape == w.x.shape
+    d = oracle.dispatch_forward(w.x.cpu(), wts, idx, E, oracle_params(w).expert)
+    check_close(out, d.out, "dispatch module 1-D indices cfg2 N=90")
 
 
 def test_dispatch_of_layer_routing_equals_layer(cuda):
@@ -144,12 +162,12 @@ def test_module_with_expert_modules(cuda, oracle, dtype):
     weight changes), [N, k] routing, collect_stats."""
     torch.manual_seed(0)
     E, H, F, N, k = 6, 256, 384, 50, 2
-    experts = nn.ModuleList([_SwiGLU(H, F, dtype, cuda) for _ in range(E)])
+    experts = nn.ModuleList([_SwiGLU(H, F, dtype, cuda) for _ in range(E)]).eval()
     x = torch.randn(N, H, device=cuda).to(dtype)
     idx, wts = _routing(N, k, E, seed=14)
     idx[idx == 5] = 4  # expert 5 unused
     idx_t, w_t = torch.from_numpy(idx).to(cuda), torch.from_numpy(wts).to(cuda)
-    m = PiscesLxFusedMoEDispatch(E, k)
+    m = PiscesLxFusedMoEDispatch(E, k).eval()
     out, stats = m(x, w_t, idx_t, experts, collect_stats=True)
     fn = lambda e: tuple(getattr(experts[e], n).weight.detach().float().cpu()
                          for n in ("gate_proj", "up_proj", "down_proj"))

@@ -6,12 +6,11 @@ capacity against the oracle's, the routing bit for bit given the GPU's fp32 logi
 the outputs against the oracle's reference forward: bf16 max-abs <= 2e-2 and cosine >=
 0.9999; fp32 max-abs <= 1e-4 and cosine >= 0.999999.
 
-bf16 tolerance: every element within max(2e-2, two bf16 ulps of the reference value), at
-most 1e-5 of the elements beyond 2e-2, cosine >= 0.9999; the raw max-abs is printed. Above
-|out| = 2 a bf16 ulp is 0.0156 (0.031 above 4), and the reference's own bf16 chain moves by up
-to 0.031 max-abs when only the fp32 summation order of its GEMMs changes (CPU measurement at
-cfg4: K summed in two halves vs one pass, 3 of 1.97M elements above 2e-2), so 2e-2 cannot
-bind every element of two correct implementations.
+bf16 tolerance (tests/helpers.py bf16_allowance): every element within 2e-2 of the oracle,
+except where |want| >= 2: two bf16 steps (0.03125) in [2, 4), where the reference's own bf16
+chain lands two steps from the correctly rounded oracle (pinned on the CPU by
+tests/test_oracle_bf16_envelope.py at cfg4, 384 tokens), and the adjacent bf16 value from 4 up;
+at most 1e-5 of the elements above 2e-2; cosine >= 0.9999. The raw max-abs is printed.
 """
 import numpy as np
 import pytest

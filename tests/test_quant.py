@@ -46,6 +46,24 @@ def test_int4_packing_order_and_groups():
     assert un[0, 0] == 15 and un[0, 128] == 1                  # +-absmax -> +-7 around 8
 
 
+def test_int4_scale_range_edges():
+    """The kernels apply an int4 group scale exactly for bf16 2^-126 <= |s| < 2^97 (and 0):
+    the quantizer and the packed-file loader reject scales outside that range."""
+    top = 2.0 ** 97 - 2.0 ** 89            # the largest bf16 below 2^97
+    w = torch.zeros(1, 128)
+    w[0, 0] = 7 * top
+    _, s = quant.quantize_int4(w)
+    assert float(s[0, 0]) == top
+    w[0, 0] = 7 * 2.0 ** 97
+    with pytest.raises(ValueError, match="outside the supported range"):
+        quant.quantize_int4(w)
+    ok = torch.tensor([0.0, 2.0 ** -126, -(2.0 ** -126), top, -top, 1e-8], dtype=torch.bfloat16)
+    quant.check_int4_scales(ok)
+    for bad in (2.0 ** 97, -(2.0 ** 97), 2.0 ** -127, -(2.0 ** -130), float("inf"), float("nan")):
+        with pytest.raises(ValueError, match="outside the supported range"):
+            quant.check_int4_scales(torch.tensor([0.5, bad], dtype=torch.bfloat16))
+
+
 def test_fp8_blocks_exact_and_clamped():
     g = torch.Generator().manual_seed(1)
     w = torch.randn(256, 384, generator=g) * 0.05
