@@ -9,7 +9,7 @@ Default workload: BASELINE configs[1] (cfg2) — W8A16 layer, hidden 4096, 64 ex
 1408), top-6, 2 shared experts, decode batch of 64 sequences x 1 token. The same run also
 times configs[2] (cfg3, the same layer on a ~16K-token ragged prefill) as the "prefill"
 object, and the CPU oracle (the reference algorithm restated in torch on the host) on cfg2
-as "cpu_baseline".
+as "cpu_baseline", with bounded samples of cfg3, cfg1, cfg4 and cfg5 beside it.
 
 roofline: the dominant kernel is the grouped expert FFN (yvmoe_expert_ffn: tile schedule,
 gate/up GEMM with SwiGLU, down GEMM); its average duration is measured with HIP events on
@@ -29,7 +29,8 @@ profiles/expert_ffn_cfg2_decode_traffic.json and reported when present.
 and prefill token counts, HBM roofline of the kernel.
 
 "other_configs": configs[0], [3], [4] (cfg1 fp32, cfg4 W4A16 mixed batch, cfg5 fp8 with skewed
-routing): layer step and grouped FFN, the FFN against both rooflines.
+routing): layer step and grouped FFN, the FFN against both rooflines; cfg5 also reports its
+realised expert load against the Zipf(1.2) target (KL).
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
        python bench.py --pmc-probe {cfg2,cfg3,moegate}   (launches only, for counter runs)
@@ -321,7 +322,7 @@ def other_configs(names, steps):
     import torch
     from pisceslx_amd import functional as yvf
     from pisceslx_amd.quant import FORMAT_NAMES
-    from pisceslx_amd.workloads import make_workload, mix_weights, router_state
+    from pisceslx_amd.workloads import load_kl, make_workload, mix_weights, router_state, zipf_target
     res = {}
     for name in names:
         w = make_workload(name, device="cuda")
@@ -341,6 +342,17 @@ def other_configs(names, steps):
                      "ffn_gbs": round(wk["bytes"] / tf / 1e9, 1),
                      "ffn_hbm_frac": round(wk["bytes"] / tf / 1e9 / HBM_PEAK_GBS, 4),
                      "active_experts": wk["active_experts"], "weights": FORMAT_NAMES[spec.fmt]}
+        if spec.zipf_s > 0:
+            counts = rt.counts.cpu().numpy()
+            target = zipf_target(spec.num_experts, spec.zipf_s, spec.zero_experts, 0)
+            res[name]["load"] = {
+                "zipf_s": spec.zipf_s, "bias_beta": spec.zipf_beta,
+                "kl_vs_zipf_nats": round(load_kl(counts, target), 4),
+                "experts_without_tokens": int((counts == 0).sum()),
+                "max_slots_per_expert": int(counts.max()),
+                "note": "KL(realised || Zipf) of the slot counts; beta minimises it "
+                        "(workloads.zipf_beta_search); top-8 caps an expert at one slot per "
+                        "token, below the heaviest Zipf shares"}
         del w, ws
         torch.cuda.empty_cache()
     return res
@@ -357,12 +369,14 @@ def cpu_model_name():
     return "unknown"
 
 
-def _cpu_time(fn, budget_s):
-    """1 warm-up, then the median of up to 3 timed runs within budget_s."""
+def _cpu_time(fn, budget_s, warmup=True, runs=3):
+    """1 warm-up (unless warmup is False), then the median of up to `runs` timed runs within
+    budget_s."""
     times = []
     t_start = time.perf_counter()
-    fn()
-    for _ in range(3):
+    if warmup:
+        fn()
+    for _ in range(runs):
         if time.perf_counter() - t_start > budget_s and times:
             break
         t0 = time.perf_counter()
@@ -371,14 +385,23 @@ def _cpu_time(fn, budget_s):
     return statistics.median(times), len(times)
 
 
-def cpu_baseline(w, x3=None, budget_s=30.0):
+# CPU baseline samples of the configurations that are not the bench line: (tokens timed,
+# warm-up, timed runs). cfg1 whole; cfg4 its first two 512-token prefill chunks; cfg5 the first
+# 2048 tokens, one timed run (about 10 s on 16 EPYC cores).
+CPU_SAMPLES = {"cfg1": (None, True, 3), "cfg4": (1024, True, 3), "cfg5": (2048, False, 1)}
+
+
+def cpu_baseline(w, x3=None, others=(), budget_s=30.0):
     """The CPU oracle (the reference algorithm restated with torch on the host: router and
-    routing, per-expert loop with experts dequantized inside it, bf16 F.linear as the reference
-    runs it, shared experts, combine) on every core this process may use, bounded. The cfg2
-    decode batch is timed whole; for cfg3 (prefill) a leading slice of the packed batch is
-    timed (the per-token cost of the full 16K-token forward, which would take minutes)."""
+    routing, per-expert loop with experts dequantized inside it, F.linear of the layer dtype as
+    the reference runs it, shared experts, combine) on every core this process may use,
+    bounded. The cfg2 decode batch is timed whole; for cfg3 (prefill) a leading slice of the
+    packed batch is timed (the per-token cost of the full 16K-token forward, which would take
+    minutes); `others` names configurations sampled as CPU_SAMPLES says (a slice is routed as a
+    batch of its own: capacity from its own token count)."""
     import torch
     from oracle import moe_oracle
+    from pisceslx_amd.workloads import make_workload
     cores = max(1, len(os.sched_getaffinity(0)))
     torch.set_num_threads(cores)
     params = moe_oracle.params_from_workload(w)
@@ -396,6 +419,22 @@ def cpu_baseline(w, x3=None, budget_s=30.0):
         res["cfg3"] = {"value": round(n_tok / t3, 2), "unit": "tokens/s",
                        "sample": f"cfg3 layer on the first {n_tok} tokens of the packed prefill "
                                  f"batch, 1 warm-up + median of {n3} runs ({t3:.3f} s each)"}
+    del params
+    for name in others:
+        n_tok, warm, runs = CPU_SAMPLES[name]
+        wo = make_workload(name, device="cuda")
+        po = moe_oracle.params_from_workload(wo)   # packed experts copied to host memory
+        xo = (wo.x if n_tok is None else wo.x[:n_tok]).cpu()
+        total = wo.n_tokens
+        del wo
+        torch.cuda.empty_cache()
+        to, no = _cpu_time(lambda: moe_oracle.layer_forward(xo, po, reference_linear=True),
+                           budget_s, warmup=warm, runs=runs)
+        what = "the whole batch" if n_tok is None else f"the first {xo.shape[0]} of {total} tokens"
+        res[name] = {"value": round(xo.shape[0] / to, 2), "unit": "tokens/s",
+                     "sample": f"{name} layer on {what}, {'1 warm-up + ' if warm else ''}median of "
+                               f"{no} run{'s' if no > 1 else ''} ({to:.3f} s each)"}
+        del po, xo
     return res
 
 
@@ -485,7 +524,8 @@ def main():
     if not args.no_other_configs:
         result["other_configs"] = other_configs(("cfg1", "cfg4", "cfg5"), max(5, args.prefill_steps // 2))
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(w, x3_cpu)
+        result["cpu_baseline"] = cpu_baseline(
+            w, x3_cpu, others=() if args.no_other_configs else ("cfg1", "cfg4", "cfg5"))
     print(json.dumps(result), flush=True)
 
 

@@ -9,7 +9,8 @@ Each configuration is a Yv MoE layer shape, a weight format and a packed ragged 
   cfg4  H5120 E128 F1536 top-8 S1 W4A16 int4 g128 (bf16 scales, zero point 8),
         8 prefill chunks of 512 + 248 decode tokens (N=4344)
   cfg5  H7168 E256 F2048 top-8 S0 fp8 e4m3fn 128x128, 8192 tokens, fixed-shape routing with
-        a per-expert bias so the load follows Zipf(1.2) and 16 experts receive no tokens
+        a per-expert bias beta * ln(p_e), p_e ~ Zipf(1.2), beta chosen so the realised load is
+        closest to Zipf(1.2) in KL, and 16 experts that receive no tokens
 
 Derivation (seeded ``torch.Generator`` on the generation device, in this order): token
 lengths, x ~ N(0,1), gate weight ~ N(0, 0.02), complexity predictor W1, W2 ~ N(0, 0.02)
@@ -43,6 +44,7 @@ class LayerSpec:
     fixed_shape_mode: bool = False
     zipf_s: float = 0.0
     zero_experts: int = 0
+    zipf_beta: float = 1.0
 
 
 SPECS = {
@@ -50,8 +52,11 @@ SPECS = {
     "cfg2": LayerSpec("cfg2", 4096, 1408, 64, 6, 2, _lib.W_INT8, torch.bfloat16),
     "cfg3": LayerSpec("cfg3", 4096, 1408, 64, 6, 2, _lib.W_INT8, torch.bfloat16),
     "cfg4": LayerSpec("cfg4", 5120, 1536, 128, 8, 1, _lib.W_INT4, torch.bfloat16),
+    # zipf_beta: the bias scale whose realised top-8 load is closest to Zipf(1.2) in KL
+    # (zipf_beta_search over 0.50 .. 2.00 in steps of 0.05 on cfg5's logits; checked by
+    # tests/test_workloads.py)
     "cfg5": LayerSpec("cfg5", 7168, 2048, 256, 8, 0, _lib.W_FP8, torch.bfloat16,
-                      fixed_shape_mode=True, zipf_s=1.2, zero_experts=16),
+                      fixed_shape_mode=True, zipf_s=1.2, zero_experts=16, zipf_beta=1.0),
 }
 
 
@@ -98,18 +103,64 @@ class Workload:
         return int(self.x.shape[0])
 
 
-def zipf_bias(E: int, s: float, zero: int, seed: int) -> np.ndarray:
-    """expert_bias_e = ln(p_e) with p_e ~ rank^-s over a seeded permutation; `zero` seeded
-    tail experts get -30 so that they receive no tokens."""
+def zipf_target(E: int, s: float, zero: int, seed: int) -> np.ndarray:
+    """Target load share of each expert: p_e ~ rank_e^-s over a seeded permutation of the
+    experts, 0 for the `zero` seeded tail experts, normalised over the others."""
+    rng = np.random.default_rng(seed)
+    order = rng.permutation(E)
+    rank = np.empty(E, dtype=np.int64)
+    rank[order] = np.arange(1, E + 1)
+    p = rank.astype(np.float64) ** (-s)
+    p[order[E - zero:]] = 0.0
+    return p / p.sum()
+
+
+def zipf_bias(E: int, s: float, zero: int, seed: int, beta: float = 1.0) -> np.ndarray:
+    """expert_bias_e = beta * ln(p_e) with p_e ~ rank^-s over a seeded permutation; `zero`
+    seeded tail experts get -30 so that they receive no tokens."""
     rng = np.random.default_rng(seed)
     order = rng.permutation(E)
     rank = np.empty(E, dtype=np.int64)
     rank[order] = np.arange(1, E + 1)
     p = rank.astype(np.float64) ** (-s)
     p /= p.sum()
-    bias = np.log(p).astype(np.float32)
+    bias = (beta * np.log(p)).astype(np.float32)
     bias[order[E - zero:]] = -30.0
     return bias
+
+
+def load_kl(counts, target: np.ndarray) -> float:
+    """KL(realised || target) in nats of an expert-load histogram (slot counts per expert)
+    against the target shares; experts with no load add nothing, load on an expert whose target
+    is 0 gives inf."""
+    c = np.asarray(counts, dtype=np.float64)
+    q = c / c.sum()
+    m = q > 0
+    if np.any(target[m] <= 0):
+        return float("inf")
+    return float((q[m] * np.log(q[m] / target[m])).sum())
+
+
+def zipf_beta_search(logits: torch.Tensor, spec: "LayerSpec", seed: int = 0,
+                     grid=None) -> tuple:
+    """The bias scale beta (on a grid, default 0.50 .. 2.00 in steps of 0.05) whose realised
+    load — top-k of logits + zipf_bias(beta), as the fixed-shape router ranks them — is closest
+    in KL to the Zipf(s) target. With top-k routing no expert can take more than one slot per
+    token, so the heaviest Zipf shares are out of reach and the KL stays above 0. Returns
+    (beta, kl)."""
+    if grid is None:
+        grid = [round(0.5 + 0.05 * i, 2) for i in range(31)]
+    E, k = spec.num_experts, spec.top_k
+    target = zipf_target(E, spec.zipf_s, spec.zero_experts, seed)
+    best = None
+    lg = logits.float()
+    for beta in grid:
+        b = torch.from_numpy(zipf_bias(E, spec.zipf_s, spec.zero_experts, seed, beta)).to(lg.device)
+        idx = torch.topk(lg + b, k, dim=1).indices.reshape(-1).cpu().numpy()
+        kl = load_kl(np.bincount(idx, minlength=E), target)
+        if best is None or kl < best[1]:
+            best = (beta, kl)
+    return best
 
 
 def make_workload(name, device="cpu", seed: int = 0, n_tokens: Optional[int] = None,
@@ -127,7 +178,8 @@ def make_workload(name, device="cpu", seed: int = 0, n_tokens: Optional[int] = N
     spec = LayerSpec(base.name, hidden or base.hidden, ffn or base.ffn,
                      num_experts or base.num_experts, min(base.top_k, num_experts or base.num_experts),
                      base.num_shared, base.fmt, base.act_dtype, base.fixed_shape_mode, base.zipf_s,
-                     min(base.zero_experts, max(0, (num_experts or base.num_experts) - base.top_k)))
+                     min(base.zero_experts, max(0, (num_experts or base.num_experts) - base.top_k)),
+                     base.zipf_beta)
     dev = torch.device(device)
     if lengths is None:
         lengths = seq_lengths(name, seed)
@@ -146,8 +198,10 @@ def make_workload(name, device="cpu", seed: int = 0, n_tokens: Optional[int] = N
     bias = None
     meta = {"seed": seed, "n_tokens": N}
     if spec.fixed_shape_mode and spec.zipf_s > 0:
-        bias = torch.from_numpy(zipf_bias(E, spec.zipf_s, spec.zero_experts, seed)).to(dev)
+        bias = torch.from_numpy(zipf_bias(E, spec.zipf_s, spec.zero_experts, seed,
+                                          spec.zipf_beta)).to(dev)
         meta["zipf_s"] = spec.zipf_s
+        meta["zipf_beta"] = spec.zipf_beta
         meta["zero_experts"] = spec.zero_experts
     pk = ExpertPacker(spec.fmt, E, S, H, Fd, dev)
     for i in range(E + S):
