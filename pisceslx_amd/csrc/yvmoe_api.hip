@@ -462,14 +462,22 @@ int32_t yvmoe_moegate_forward(const void* x, int32_t act_dtype, int32_t n_tokens
                "workspace %zu bytes, need %zu", workspace_bytes, need);
     hipStream_t st = (hipStream_t)stream;
     char* ws = (char*)workspace;
-    rc = moegate_launch(x, act_dtype, n_tokens, gate, modal_id, logits, loss, ws + rbytes, st);
+    // decode sizes: the per-token kernel also runs each token's top-k, and the small-batch
+    // routing kernel reduces the loss (two launches fewer)
+    const bool small = route_small_fixed(n_tokens);
+    const GateTopk tk = route_topk_outputs(n_tokens, E, top_k, routing, ws);
+    bool topk_done = false;
+    GateLossArgs la{};
+    rc = moegate_launch(x, act_dtype, n_tokens, gate, modal_id, logits, loss, ws + rbytes, st,
+                        small ? &tk : nullptr, &topk_done, small ? &la : nullptr);
     if (rc) return rc;
     yvmoe_router r{};
     r.num_experts = E;
     r.hidden = gate->hidden;
     r.top_k = top_k;
     r.fixed_shape_mode = 1;
-    return route_launch(n_tokens > 0 ? logits : nullptr, E, nullptr, E, n_tokens, &r, -1, routing, ws, st);
+    return route_launch(n_tokens > 0 ? logits : nullptr, E, nullptr, E, n_tokens, &r, -1, routing, ws, st,
+                        1, 0, nullptr, topk_done, small ? &la : nullptr);
 }
 
 static size_t forward_moegate_bytes(int N, int act, int k, const yvmoe_moegate* g,
@@ -525,15 +533,23 @@ int32_t yvmoe_forward_moegate(const void* x, int32_t act_dtype, int32_t n_tokens
     char* ws = (char*)workspace;
     const int N = n_tokens;
     const size_t rbytes = route_ws(N, E, k).bytes;
-    // the gate's region is reused by the expert FFN once the routing has been computed
-    rc = moegate_launch(x, act_dtype, N, gate, modal_id, logits, loss, ws + rbytes, st);
+    // the gate's region is reused by the expert FFN once the routing has been computed (the
+    // loss reduction, deferred to the routing kernel at decode sizes, reads it first). At decode
+    // sizes the per-token kernel also runs each token's top-k, unless the routing comes from a
+    // cached PathMoE stage's logits.
+    const bool small = route_small_fixed(N);
+    const GateTopk tk = route_topk_outputs(N, E, k, routing, ws);
+    bool topk_done = false;
+    GateLossArgs la{};
+    rc = moegate_launch(x, act_dtype, N, gate, modal_id, logits, loss, ws + rbytes, st,
+                        (small && route_logits == nullptr) ? &tk : nullptr, &topk_done,
+                        small ? &la : nullptr);
     if (rc) return rc;
     yvmoe_router r{};
     r.num_experts = E;
     r.hidden = gate->hidden;
     r.top_k = k;
     r.fixed_shape_mode = 1;
-    const bool small = N > 0 && N <= kSmallRouteTok;
     TileTable tiles{};
     if (small)
         tiles = ffn_tile_table(N, k, E, S, experts->ffn, act_dtype,
@@ -542,7 +558,7 @@ int32_t yvmoe_forward_moegate(const void* x, int32_t act_dtype, int32_t n_tokens
                                ws);
     const float* lsrc = route_logits != nullptr ? route_logits : logits;
     rc = route_launch(N > 0 ? lsrc : nullptr, E, nullptr, E, N, &r, -1, routing, ws, st, 1, 0,
-                      small ? &tiles : nullptr);
+                      small ? &tiles : nullptr, topk_done, small ? &la : nullptr);
     if (rc) return rc;
     if (N == 0) return YVMOE_OK;
     void* y = ws + rbytes + ffn_ws(N, k, E, S, experts->ffn, act_dtype).bytes;

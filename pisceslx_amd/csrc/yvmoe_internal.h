@@ -210,13 +210,42 @@ inline int tile_fold(int N, int k, int E) {
     return (mean > 256 && mean <= 256 + 2 * kTileFold) ? kTileFold : 0;
 }
 
+// YvMoEGate loss inputs (the per-work-group sums of the per-token kernels) for the kernel that
+// reduces them (yvmoe_gate_loss.h): the loss kernel, or the small-batch routing kernel when it
+// runs next on the stream.
+struct GateLossArgs {
+    const float* part;  // [E + 2][G]
+    int G, E, N;
+    float lb_alpha, z_alpha, budget, cap_loss;
+    int has_soft;
+    float* loss;
+};
+// The YvMoEGate per-token kernel's own top-k (decode sizes, at most 64 experts): the per-slot
+// outputs of route_topk_small_kernel, in the routing workspace and indices.
+struct GateTopk {
+    int64_t* idx;
+    float* topp;
+    float* w0;
+    int k;
+};
+
 // routing (yvmoe_route.hip). Logits (and predictor columns) are the in-order sum of ksplit
 // partial copies split_stride floats apart (ksplit = 1: plain logits). With tiles non-null
 // (small batches only) the tile table is built as well.
+// topk_ready (small batches in fixed-shape mode): the per-token top-k outputs are already in
+// place (the YvMoEGate per-token kernel wrote them), so only route_small_kernel runs; with
+// loss set (small batches) that kernel also reduces the YvMoEGate loss.
 int route_launch(const float* logits, int ld, const float* pred, int pred_ld, int N,
                  const yvmoe_router* r, int cap_override, yvmoe_routing* out, char* ws,
                  hipStream_t st, int ksplit = 1, long long split_stride = 0,
-                 const TileTable* tiles = nullptr);
+                 const TileTable* tiles = nullptr, bool topk_ready = false,
+                 const GateLossArgs* loss = nullptr);
+// The per-slot top-k outputs of route_launch's small-batch path for this routing (where
+// route_topk_small_kernel writes them).
+GateTopk route_topk_outputs(int N, int E, int k, yvmoe_routing* out, char* ws);
+// Whether route_launch takes the small-batch path (route_small_kernel) for a fixed-shape
+// routing of N tokens.
+inline bool route_small_fixed(int N) { return N > 0 && N <= kSmallRouteTok; }
 // external routing of the dispatch entry (yvmoe_route.hip): counts, offsets, the stable
 // permutation and its inverse (pos = -1 for ids outside [0, E)), the invalid-slot count, and
 // with w32 set the bf16 weights widened to fp32.
@@ -253,8 +282,13 @@ struct GateWs {
 int moegate_heads_rows(const yvmoe_moegate* g);
 int moegate_proj_rows(const yvmoe_moegate* g);
 GateWs gate_ws(int N, int act, const yvmoe_moegate* g);
+// topk (optional): the per-token kernel also runs each token's top-k (E <= 64 and the
+// work-group-per-token form only; returns whether it did). defer_loss (optional): the loss
+// reduction is not launched; its arguments are returned for the caller's next kernel.
 int moegate_launch(const void* x, int act, int N, const yvmoe_moegate* g, const int* modal_id,
-                   float* logits, float* loss, char* ws, hipStream_t st);
+                   float* logits, float* loss, char* ws, hipStream_t st,
+                   const GateTopk* topk = nullptr, bool* topk_done = nullptr,
+                   GateLossArgs* defer_loss = nullptr);
 // RMSNorm (yvmoe_norm.hip): nn (1 or 2) norms in sequence, one wavefront per row; y may alias x.
 struct NormChain {
     const void* w[2];

@@ -20,6 +20,8 @@
 #include <algorithm>
 
 #include "yvmoe_internal.h"
+#include "yvmoe_gate_loss.h"
+#include "yvmoe_topk.h"
 
 namespace yvmoe {
 namespace {
@@ -51,6 +53,8 @@ struct GateArgs {
     int E, D, N, mask;
     float* logits;
     float* part;  // [E + 2][G]
+    int do_topk;  // E <= 64: also the token's top-k (route_topk_small_kernel's outputs)
+    GateTopk tk;
 };
 
 // Rotation by O lanes inside each row of 16 lanes (DPP row_ror).
@@ -252,6 +256,21 @@ __device__ RadixPick radix_select(KeyFn key, unsigned R, unsigned* hist, unsigne
 //      select over the indices when the sel_k-th value is tied;
 //   3. each candidate's rank in (value descending, index ascending) order places it: ranks
 //      below sel_k are kept, in that order (ties at the threshold keep the lower indices).
+// Top-k of one token whose logits (at most 64 experts) are in LDS, by the first 16 lanes of a
+// wavefront: route_topk_small_kernel's outputs for the token. Not inlined: its registers would
+// otherwise add to the per-token kernel's, which then spills.
+__device__ __noinline__ void token_topk(const float* s_rl, int lane, int E, GateTopk tk, int t) {
+    int my_id;
+    float my_ts, my_w0;
+    topk_token<4>([&](int e) { return s_rl[e]; }, nullptr, lane, E, tk.k, my_id, my_ts, my_w0);
+    if (lane < tk.k) {
+        const size_t sl = (size_t)t * tk.k + lane;
+        tk.idx[sl] = (int64_t)my_id;
+        tk.topp[sl] = my_ts;
+        tk.w0[sl] = my_w0;
+    }
+}
+
 template <int NT, int NS, int J4>
 __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
     constexpr int Q = NT / 256;    // threads per output of the split dot products
@@ -273,6 +292,7 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
     __shared__ float red[2][NT / 64];
     __shared__ unsigned ctl[8];
     __shared__ float s_med, s_tlb;
+    __shared__ float s_rl[64];  // the token's logits for its top-k (do_topk)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = a.E, D = a.D, K = a.sel_k;
     const bool is_e = tid < E;
@@ -540,6 +560,17 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
                     soft_tot = wave_sum(sv);
                 }
                 const float l = is_e ? logit(soft) : 0.f;
+                if (a.do_topk) {
+                    // the routing of this token from the logits just written (the bit-exact
+                    // top-k of the routing kernels): the wavefront's 64 logits through LDS to its
+                    // first 16 lanes, which hold experts l, l + 16, ... as topk_token expects
+                    s_rl[tid] = l;
+                    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                    __builtin_amdgcn_wave_barrier();
+                    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                    if (lane < kLanes) token_topk(s_rl, lane, E, a.tk, t);
+                    __builtin_amdgcn_wave_barrier();  // s_rl is rewritten by the next token
+                }
                 const float lm = wave_max(is_e ? l : -INFINITY);
                 const float le = is_e ? expf(l - lm) : 0.f;
                 const float ls = wave_sum(le);
@@ -906,65 +937,8 @@ __global__ __launch_bounds__(64 * kWaveTok) void moegate_wave_kernel(GateArgs a)
     }
 }
 
-// loss = alpha · Σ_e (mean_n score - 1/E)² + capacity term + z_alpha · mean(logits²)
-//        + 0.01 · (mean_n Σ_e soft - budget)²   (gate.py:433-444, :556-610)
-// Column c of the per-work-group sums is summed by P threads (contiguous group ranges, 32
-// loads in flight each) and the P partial sums in order; the load-balance sum over experts is
-// one wave reduction per wave and the waves in order.
-__global__ __launch_bounds__(1024) void moegate_loss_kernel(const float* __restrict__ part, int G,
-                                                            int E, int N, float lb_alpha,
-                                                            float z_alpha, float budget,
-                                                            float cap_loss, int has_soft,
-                                                            float* __restrict__ loss) {
-    __shared__ float psum[1024];
-    __shared__ float col[YVMOE_MAX_EXPERTS + 2];
-    __shared__ float red[16];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    int cp = 1;
-    while (cp < E + 2) cp <<= 1;
-    const int P = 1024 / cp;  // threads per column (>= 2: E + 2 <= 258)
-    const int c = tid / P, p = tid % P;
-    const int chunk = (G + P - 1) / P;
-    float sum = 0.f;
-    if (c < E + 2) {
-        const float* pc = part + (long long)c * G;
-        const int g1 = min(G, (p + 1) * chunk);
-        for (int g0 = p * chunk; g0 < g1; g0 += 32) {
-            float v[32];
-#pragma unroll
-            for (int i = 0; i < 32; ++i) v[i] = g0 + i < g1 ? pc[g0 + i] : 0.f;
-#pragma unroll
-            for (int i = 0; i < 32; ++i) sum += v[i];
-        }
-    }
-    psum[tid] = sum;
-    __syncthreads();
-    if (tid < E + 2) {
-        float s = psum[tid * P];
-        for (int i = 1; i < P; ++i) s += psum[tid * P + i];
-        col[tid] = s;
-    }
-    __syncthreads();
-    const float fn = (float)N;
-    float d = 0.f;
-    if (tid < E) {
-        d = col[tid] / fn - 1.f / (float)E;
-        d = d * d;
-    }
-    d = wave_sum(d);
-    if (lane == 0) red[wave] = d;
-    __syncthreads();
-    if (tid == 0) {
-        float lb = red[0];
-        for (int w = 1; w < 16; ++w) lb += red[w];
-        float total = lb_alpha * lb + cap_loss + z_alpha * (col[E] / ((float)N * (float)E));
-        if (has_soft) {
-            const float ac = col[E + 1] / fn - budget;
-            total += 0.01f * (ac * ac);
-        }
-        loss[0] = total;
-    }
-}
+// The loss from the per-work-group sums (yvmoe_gate_loss.h), in a launch of its own.
+__global__ __launch_bounds__(1024) void moegate_loss_kernel(GateLossArgs a) { gate_loss_block(a); }
 
 }  // namespace
 
@@ -987,7 +961,9 @@ GateWs gate_ws(int N, int act, const yvmoe_moegate* g) {
 }
 
 int moegate_launch(const void* x, int act, int N, const yvmoe_moegate* g, const int* modal_id,
-                   float* logits, float* loss, char* ws, hipStream_t st) {
+                   float* logits, float* loss, char* ws, hipStream_t st, const GateTopk* topk,
+                   bool* topk_done, GateLossArgs* defer_loss) {
+    if (topk_done != nullptr) *topk_done = false;
     const GateWs w = gate_ws(N, act, g);
     const int E = g->num_experts, H = g->hidden;
     const int P = moegate_proj_rows(g);
@@ -1047,6 +1023,11 @@ int moegate_launch(const void* x, int act, int N, const yvmoe_moegate* g, const 
             moegate_wave_kernel<1><<<groups, 64 * kWaveTok, eo_bytes, st>>>(a);
             YV_LAUNCH_CHECK("moegate_wave");
         } else {
+            if (topk != nullptr && E <= 64) {
+                a.do_topk = 1;
+                a.tk = *topk;
+                if (topk_done != nullptr) *topk_done = true;
+            }
 #define YV_TOK(NS, J4) moegate_token_kernel<1024, NS, J4><<<w.groups, 1024, 0, st>>>(a)
         switch (j4 * 10 + a.nsplit) {
             case 11: YV_TOK(1, 1); break;
@@ -1062,9 +1043,13 @@ int moegate_launch(const void* x, int act, int N, const yvmoe_moegate* g, const 
         YV_LAUNCH_CHECK("moegate_token");
         }
     }
-    moegate_loss_kernel<<<1, 1024, 0, st>>>(part, groups, E, N, g->load_balance_alpha,
-                                           g->z_loss_alpha, g->soft_budget, g->capacity_loss,
-                                           (g->heads & YVMOE_HEAD_SOFT) ? 1 : 0, loss);
+    const GateLossArgs la{part, groups, E, N, g->load_balance_alpha, g->z_loss_alpha, g->soft_budget,
+                          g->capacity_loss, (g->heads & YVMOE_HEAD_SOFT) ? 1 : 0, loss};
+    if (defer_loss != nullptr) {
+        *defer_loss = la;
+        return YVMOE_OK;
+    }
+    moegate_loss_kernel<<<1, 1024, 0, st>>>(la);
     YV_LAUNCH_CHECK("moegate_loss");
     return YVMOE_OK;
 }
