@@ -310,11 +310,13 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
                                ffn_tile_rows(act_dtype, N, k, E, experts->hidden, experts->ffn,
                                              experts->format),
                                ws);
+    // the routing kernel builds the tile table unless it has a light part (the FFN builds that)
+    const bool tiles_by_route = small && tiles.light == 0;
     rc = route_launch(lsrc, ld, need_pred ? lsrc + pad16(E) : nullptr, ld, N, router, -1, routing,
-                      ws, st, split ? ks : 1, (long long)N * ld, small ? &tiles : nullptr);
+                      ws, st, split ? ks : 1, (long long)N * ld, tiles_by_route ? &tiles : nullptr);
     if (rc) return rc;
     if (N == 0) return YVMOE_OK;
-    rc = expert_ffn_launch(x, act_dtype, N, k, experts, routing, y, ws, st, small);
+    rc = expert_ffn_launch(x, act_dtype, N, k, experts, routing, y, ws, st, tiles_by_route);
     if (rc) return rc;
     return combine_launch(y, act_dtype, N, experts->hidden, k, experts->num_shared, routing, mix,
                           skip, out, shared_out, st);
@@ -557,12 +559,13 @@ int32_t yvmoe_forward_moegate(const void* x, int32_t act_dtype, int32_t n_tokens
                                              experts->format),
                                ws);
     const float* lsrc = route_logits != nullptr ? route_logits : logits;
+    const bool tiles_by_route = small && tiles.light == 0;
     rc = route_launch(N > 0 ? lsrc : nullptr, E, nullptr, E, N, &r, -1, routing, ws, st, 1, 0,
-                      small ? &tiles : nullptr, topk_done, small ? &la : nullptr);
+                      tiles_by_route ? &tiles : nullptr, topk_done, small ? &la : nullptr);
     if (rc) return rc;
     if (N == 0) return YVMOE_OK;
     void* y = ws + rbytes + ffn_ws(N, k, E, S, experts->ffn, act_dtype).bytes;
-    rc = expert_ffn_launch(x, act_dtype, N, k, experts, routing, y, ws, st, small);
+    rc = expert_ffn_launch(x, act_dtype, N, k, experts, routing, y, ws, st, tiles_by_route);
     if (rc) return rc;
     return combine_launch(y, act_dtype, N, experts->hidden, k, S, routing, mix, skip, out,
                           shared_out, st);

@@ -1444,17 +1444,22 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(GemmParams p) {
 
 // --------------------------------------------------------------- tile schedule
 // Segments: routed experts [0, E) from the routing offsets, then S shared experts of N
-// rows each after the N*k routed rows. Every segment is cut into 64-row tiles.
+// rows each after the N*k routed rows. Every segment is cut into tile_rows-row tiles (seg_tiles);
+// with light > 0 a remainder of at most light rows goes to the light table instead (seg_light).
 __global__ __launch_bounds__(512) void build_tiles_kernel(const int* __restrict__ offsets, int E,
                                                           int S, int N, int k, int tile_rows,
                                                           int fold, int* __restrict__ seg,
                                                           int* __restrict__ tile_seg,
                                                           int* __restrict__ tile_row0,
-                                                          int* __restrict__ ntiles) {
+                                                          int* __restrict__ ntiles, int light,
+                                                          int* __restrict__ ltile_seg,
+                                                          int* __restrict__ ltile_row0,
+                                                          int* __restrict__ lntiles) {
     __shared__ int sc[512];
+    __shared__ int lc[512];
     const int tid = threadIdx.x;
     const int nseg = E + S;
-    int s0 = 0, s1 = 0, nt = 0;
+    int s0 = 0, s1 = 0, nt = 0, nl = 0;
     if (tid < nseg) {
         if (tid < E) {
             s0 = offsets[tid];
@@ -1465,14 +1470,18 @@ __global__ __launch_bounds__(512) void build_tiles_kernel(const int* __restrict_
         }
         seg[tid] = s0;
         if (tid == nseg - 1) seg[nseg] = s1;
-        nt = seg_tiles(s1 - s0, tile_rows, fold);
+        nt = seg_tiles(s1 - s0, tile_rows, fold, light);
+        nl = light > 0 ? seg_light(s1 - s0, tile_rows, light) : 0;
     }
     sc[tid] = nt;
+    lc[tid] = nl;
     __syncthreads();
     for (int o = 1; o < 512; o <<= 1) {
-        int v = (tid >= o) ? sc[tid - o] : 0;
+        const int v = (tid >= o) ? sc[tid - o] : 0;
+        const int u = (tid >= o) ? lc[tid - o] : 0;
         __syncthreads();
         sc[tid] += v;
+        lc[tid] += u;
         __syncthreads();
     }
     if (tid < nseg) {
@@ -1481,8 +1490,15 @@ __global__ __launch_bounds__(512) void build_tiles_kernel(const int* __restrict_
             tile_seg[start + q] = tid;
             tile_row0[start + q] = s0 + q * tile_rows;
         }
+        if (nl) {  // the remainder after the segment's full tiles
+            ltile_seg[lc[tid] - 1] = tid;
+            ltile_row0[lc[tid] - 1] = s0 + ((s1 - s0) / tile_rows) * tile_rows;
+        }
     }
-    if (tid == 511) *ntiles = sc[511];
+    if (tid == 511) {
+        *ntiles = sc[511];
+        if (light > 0) *lntiles = lc[511];
+    }
 }
 
 // --------------------------------------------------------------- combine
@@ -1910,6 +1926,10 @@ TileTable ffn_tile_table(int N, int k, int E, int S, int F, int act, int tile_ro
     t.S = S;
     t.tile_rows = tile_rows;
     t.fold = tile_rows == TBM ? tile_fold(N, k, E) : 0;
+    t.light = tile_rows == TBM ? tile_light(N, k, E, t.fold) : 0;
+    t.ltile_seg = (int*)(fws + FL.lseg);
+    t.ltile_row0 = (int*)(fws + FL.lrow0);
+    t.lntiles = (int*)(fws + FL.lntiles);
     return t;
 }
 
@@ -1931,10 +1951,23 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     const int T = max_tiles(N, k, E, S, tile_rows);
     if (!tiles_ready) {
         build_tiles_kernel<<<1, 512, 0, st>>>(routing->offsets, E, S, N, k, tile_rows, tt.fold, seg,
-                                              tile_seg, tile_row0, ntiles);
+                                              tile_seg, tile_row0, ntiles, tt.light, tt.ltile_seg,
+                                              tt.ltile_row0, tt.lntiles);
         YV_LAUNCH_CHECK("build_tiles");
+    } else if (tt.light > 0) {
+        set_error("internal: a light tile table is built by the FFN launch itself");
+        return YVMOE_ERR_ARG;
     }
     const int wf = w->format;
+    // the light table's remainders (at most kLightRows rows, one per segment) on the streaming
+    // form, after the main table's launch of the same GEMM
+    auto light_launch = [&](GemmParams q, auto epi, const char* name) {
+        constexpr int EPIV = decltype(epi)::value;
+        q.tile_seg = tt.ltile_seg;
+        q.tile_row0 = tt.ltile_row0;
+        q.ntiles = tt.lntiles;
+        return stream_dispatch<EPIV, 2, 1, kLightRows / 16, true, 4>(wf, q, E + S, st, name);
+    };
     GemmParams p{};
     p.tile_seg = tile_seg;
     p.tile_row0 = tile_row0;
@@ -1966,6 +1999,10 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
                        : gemm_dispatch<EPI_SWIGLU>(act, wf, p, T, (F % 32 == 0) ? 2 : 1, 1, st,
                                                    "expert_gemm1", maxrb);
     if (rc != YVMOE_OK) return rc;
+    if (tt.light > 0) {
+        rc = light_launch(p, std::integral_constant<int, EPI_SWIGLU>{}, "expert_gemm1_light");
+        if (rc != YVMOE_OK) return rc;
+    }
     // GEMM2: y = h Wd^T (rows already in sorted order)
     p.A = hbuf;
     p.lda = F;
@@ -1983,7 +2020,11 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.out = y;
     p.ldo = H;
     p.kchunk = F;
-    if (tiled) return tile_dispatch<EPI_DOWN>(wf, p, T, st, "expert_gemm2", tt.fold > 0);
+    if (tiled) {
+        rc = tile_dispatch<EPI_DOWN>(wf, p, T, st, "expert_gemm2", tt.fold > 0);
+        if (rc != YVMOE_OK || tt.light == 0) return rc;
+        return light_launch(p, std::integral_constant<int, EPI_DOWN>{}, "expert_gemm2_light");
+    }
     return streaming ? stream_dispatch<EPI_DOWN, YV_U2, YV_NB2, 1, YV_PF2, YV_WV2>(wf, p, T, st, "expert_gemm2")
                      : gemm_dispatch<EPI_DOWN>(act, wf, p, T, (H % 32 == 0) ? 2 : 1, 1, st,
                                                "expert_gemm2", maxrb);

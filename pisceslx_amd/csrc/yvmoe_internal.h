@@ -114,7 +114,7 @@ struct RouteWs {
     size_t topp, w0, allowed, blockhist, blockoff, blocksum, score, bytes;
 };
 struct FfnWs {
-    size_t seg, tile_seg, tile_row0, ntiles, h, bytes;
+    size_t seg, tile_seg, tile_row0, ntiles, lseg, lrow0, lntiles, h, bytes;
 };
 
 inline RouteWs route_ws(int N, int E, int k) {
@@ -142,6 +142,9 @@ inline FfnWs ffn_ws(int N, int k, int E, int S, int F, int act) {
     w.tile_seg = o;  o = align_up(o + (size_t)T * 4 + 4, 256);
     w.tile_row0 = o; o = align_up(o + (size_t)T * 4 + 4, 256);
     w.ntiles = o;    o = align_up(o + 4, 256);
+    w.lseg = o;      o = align_up(o + (size_t)(E + S) * 4 + 4, 256);  // light tiles (one per segment)
+    w.lrow0 = o;     o = align_up(o + (size_t)(E + S) * 4 + 4, 256);
+    w.lntiles = o;   o = align_up(o + 4, 256);
     const size_t esz = act == YVMOE_ACT_BF16 ? 2 : 4;
     w.h = o;         o = align_up(o + R * (size_t)F * esz, 256);
     w.bytes = o;
@@ -180,7 +183,10 @@ inline DispatchWs dispatch_ws(int N, int k, int E, int H, int F, int act) {
 // Tile table of the expert GEMMs (segments = E routed experts, then S shared experts of N
 // rows each; every segment cut into tile_rows-row tiles), in the FFN workspace region. With
 // fold > 0 a segment's remainder of at most fold rows joins its last full tile (which then
-// holds tile_rows + remainder rows) instead of taking a tile of its own.
+// holds tile_rows + remainder rows) instead of taking a tile of its own. With light > 0 a
+// remainder of at most light rows takes no tile of the main table but one of the light table
+// (ltile_seg, ltile_row0, lntiles: at most one per segment), which the weight-streaming GEMM
+// form runs with kLightRows-row tiles. fold and light are never both set.
 struct TileTable {
     int* seg;
     int* tile_seg;
@@ -189,16 +195,39 @@ struct TileTable {
     int S;
     int tile_rows;
     int fold;
+    int light;
+    int* ltile_seg;
+    int* ltile_row0;
+    int* lntiles;
 };
 
 // Rows the LDS-tiled GEMM form can take beyond its 256-row tile: an expert's remainder of up
 // to this many rows is folded into its last full tile.
 constexpr int kTileFold = 32;
 
-// Tiles of a segment of `rows` rows (the rule both tile-table builders follow).
-__host__ __device__ inline int seg_tiles(int rows, int tile_rows, int fold) {
+// Tiles of a segment of `rows` rows in the main table (the rule both tile-table builders
+// follow), and whether its remainder takes a light tile instead.
+__host__ __device__ inline int seg_tiles(int rows, int tile_rows, int fold, int light = 0) {
     const int n = rows / tile_rows, rem = rows - n * tile_rows;
-    return n + ((rem > 0 && !(n > 0 && rem <= fold)) ? 1 : 0);
+    return n + ((rem > 0 && !(n > 0 && rem <= fold) && rem > light) ? 1 : 0);
+}
+__host__ __device__ inline int seg_light(int rows, int tile_rows, int light) {
+    const int rem = rows % tile_rows;
+    return (rem > 0 && rem <= light) ? 1 : 0;
+}
+
+// Rows of a light tile: the weight-streaming form's 32-row tile (cfg5 FFN, one box: 256-row
+// tiles only 7.62-7.65 ms; light tiles of 16, 32, 64 rows 7.45-7.50, 7.19-7.21, 7.37 ms).
+constexpr int kLightRows = 32;
+
+// Whether the LDS-tiled expert GEMMs send remainders of at most kLightRows rows to the
+// weight-streaming form: when experts hold few tiles each (a mean under two 256-row tiles) and
+// remainders are not folded. A 256-row tile that holds a few dozen rows still streams and
+// dequantizes the expert's weights through LDS, at about half the cost of a full tile; the
+// streaming form reads them once from HBM with no LDS round trip for the weights.
+inline int tile_light(int N, int k, int E, int fold) {
+    const long long mean = (long long)N * k / (E > 0 ? E : 1);
+    return (fold == 0 && mean < 512) ? kLightRows : 0;
 }
 
 // Whether the LDS-tiled expert GEMMs fold remainders: when the mean expert holds one tile and

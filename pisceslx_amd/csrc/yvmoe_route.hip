@@ -825,6 +825,7 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
         if (tiles) {
             YV_REQUIRE(tiles->tile_rows > 0 && (tiles->tile_rows & (tiles->tile_rows - 1)) == 0,
                        YVMOE_ERR_ARG, "tile rows %d not a power of two", tiles->tile_rows);
+            YV_REQUIRE(tiles->light == 0, YVMOE_ERR_ARG, "internal: light tile tables are built by the FFN");
             a.tiles = *tiles;
         }
         if (loss != nullptr) {

@@ -167,6 +167,34 @@ def test_tiled_folded_remainders(cuda, oracle, fmt, hidden):
     assert routing.counts.cpu().tolist() == counts
 
 
+@pytest.mark.parametrize("fmt,hidden", [("int8", 256), ("int4", 256), ("fp8", 256), ("bf16", 256),
+                                        ("fp8", 1024)])
+def test_tiled_light_remainders(cuda, oracle, fmt, hidden):
+    """Skewed prefill-sized batches (mean under two 256-row tiles per expert, no folding): an
+    expert's remainder of at most 32 rows runs on the weight-streaming form with 32-row tiles
+    after the LDS-tiled launch (segments of 10 and 32 rows, and 256 + 24, 256 + 32 and the
+    shared segment's 6 x 256 + 20), a longer remainder keeps its 256-row tile (33, 57, 512 + 88),
+    and a segment of exactly 256 rows has no remainder; forced through one-hot gate rows."""
+    from pisceslx_amd import _lib
+    from pisceslx_amd.workloads import LayerSpec
+    counts = [10, 32, 33, 256, 280, 288, 600, 57]
+    E, H, F, N = len(counts), hidden, 256, sum(counts)
+    assert N == 6 * 256 + 20
+    spec = LayerSpec("light", H, F, E, 1, 1, getattr(_lib, "W_" + fmt.upper()), torch.bfloat16,
+                     fixed_shape_mode=True)
+    w = make_workload(spec, device="cuda", lengths=[N])
+    g = torch.Generator().manual_seed(6)
+    expert = torch.repeat_interleave(torch.arange(E), torch.tensor(counts))[torch.randperm(N, generator=g)]
+    x = torch.randn(N, H, generator=g) * 0.5
+    x[torch.arange(N), expert] += 8.0
+    gate = torch.zeros(E, H)
+    gate[torch.arange(E), torch.arange(E)] = 1.0
+    w.x = x.to(torch.bfloat16).cuda()
+    w.gate_weight = gate.to(torch.bfloat16).cuda()
+    _, _, routing = _run_and_check(oracle, w, label=f"layer light remainders {fmt} H={hidden} N={N}")
+    assert routing.counts.cpu().tolist() == counts
+
+
 def _shared_spec(fmt_name, S):
     from pisceslx_amd import _lib
     from pisceslx_amd.workloads import LayerSpec
