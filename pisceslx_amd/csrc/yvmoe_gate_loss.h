@@ -5,9 +5,10 @@
 // Run by one work-group of 1024 threads: its own kernel after the per-token kernels
 // (yvmoe_moegate.hip), or the tail of the small-batch routing kernel (yvmoe_route.hip), which
 // runs next on the stream at decode sizes — the same arithmetic either way. Column c is summed
-// by P threads (contiguous group ranges, 32 loads in flight each) and the P partial sums in
-// order; the load-balance sum over experts is one wave reduction per wave and the waves in
-// order.
+// by one wavefront (lane l takes groups l, l + 64, ... in order, then a wave reduction: the
+// loads of a step are one coalesced 256-byte row; the earlier layout, P threads per column over
+// contiguous group ranges, made every load touch 64 cache lines and took 35 us at 1024 groups);
+// the load-balance sum over experts is one wave reduction per wave and the waves in order.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -32,34 +33,27 @@ __device__ __forceinline__ float gl_wave_sum(float v) {
 
 // Every thread of the 1024-thread work-group calls this (it holds barriers).
 __device__ __forceinline__ void gate_loss_block(const GateLossArgs& a) {
-    __shared__ float psum[1024];
     __shared__ float col[YVMOE_MAX_EXPERTS + 2];
     __shared__ float red[16];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = a.E, G = a.G;
-    int cp = 1;
-    while (cp < E + 2) cp <<= 1;
-    const int P = 1024 / cp;  // threads per column (>= 2: E + 2 <= 258)
-    const int c = tid / P, p = tid % P;
-    const int chunk = (G + P - 1) / P;
-    float sum = 0.f;
-    if (c < E + 2) {
+    // column c by wavefront c % 16: lane l sums groups l, l + 64, ... in order (coalesced
+    // loads, 16 in flight), then the wave reduction
+    for (int c = wave; c < E + 2; c += 16) {
         const float* pc = a.part + (long long)c * G;
-        const int g1 = min(G, (p + 1) * chunk);
-        for (int g0 = p * chunk; g0 < g1; g0 += 32) {
-            float v[32];
+        float sum = 0.f;
+        for (int g0 = 0; g0 < G; g0 += 64 * 16) {
+            float v[16];
 #pragma unroll
-            for (int i = 0; i < 32; ++i) v[i] = g0 + i < g1 ? pc[g0 + i] : 0.f;
+            for (int i = 0; i < 16; ++i) {
+                const int g = g0 + 64 * i + lane;
+                v[i] = g < G ? pc[g] : 0.f;
+            }
 #pragma unroll
-            for (int i = 0; i < 32; ++i) sum += v[i];
+            for (int i = 0; i < 16; ++i) sum += v[i];
         }
-    }
-    psum[tid] = sum;
-    __syncthreads();
-    if (tid < E + 2) {
-        float s = psum[tid * P];
-        for (int i = 1; i < P; ++i) s += psum[tid * P + i];
-        col[tid] = s;
+        sum = gl_wave_sum(sum);
+        if (lane == 0) col[c] = sum;
     }
     __syncthreads();
     const float fn = (float)a.N;
