@@ -1471,7 +1471,7 @@ __global__ __launch_bounds__(512) void build_tiles_kernel(const int* __restrict_
         seg[tid] = s0;
         if (tid == nseg - 1) seg[nseg] = s1;
         nt = seg_tiles(s1 - s0, tile_rows, fold, light);
-        nl = light > 0 ? seg_light(s1 - s0, tile_rows, light) : 0;
+        nl = seg_light(s1 - s0, tile_rows, fold, light);
     }
     sc[tid] = nt;
     lc[tid] = nl;
@@ -1959,14 +1959,15 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
         return YVMOE_ERR_ARG;
     }
     const int wf = w->format;
-    // the light table's remainders (at most kLightRows rows, one per segment) on the streaming
-    // form, after the main table's launch of the same GEMM
+    // the light table's remainders (at most tt.light rows, one per segment) on the streaming
+    // form with tt.light-row tiles, after the main table's launch of the same GEMM
     auto light_launch = [&](GemmParams q, auto epi, const char* name) {
         constexpr int EPIV = decltype(epi)::value;
         q.tile_seg = tt.ltile_seg;
         q.tile_row0 = tt.ltile_row0;
         q.ntiles = tt.lntiles;
-        return stream_dispatch<EPIV, 2, 1, kLightRows / 16, true, 4>(wf, q, E + S, st, name);
+        if (tt.light > 32) return stream_dispatch<EPIV, 2, 1, 4, true, 4>(wf, q, E + S, st, name);
+        return stream_dispatch<EPIV, 2, 1, 2, true, 4>(wf, q, E + S, st, name);
     };
     GemmParams p{};
     p.tile_seg = tile_seg;

@@ -184,9 +184,9 @@ inline DispatchWs dispatch_ws(int N, int k, int E, int H, int F, int act) {
 // rows each; every segment cut into tile_rows-row tiles), in the FFN workspace region. With
 // fold > 0 a segment's remainder of at most fold rows joins its last full tile (which then
 // holds tile_rows + remainder rows) instead of taking a tile of its own. With light > 0 a
-// remainder of at most light rows takes no tile of the main table but one of the light table
-// (ltile_seg, ltile_row0, lntiles: at most one per segment), which the weight-streaming GEMM
-// form runs with kLightRows-row tiles. fold and light are never both set.
+// remainder of at most light rows that is not folded takes no tile of the main table but one of
+// the light table (ltile_seg, ltile_row0, lntiles: at most one per segment), which the
+// weight-streaming GEMM form runs with light-row tiles (32 or 64).
 struct TileTable {
     int* seg;
     int* tile_seg;
@@ -207,27 +207,35 @@ constexpr int kTileFold = 32;
 
 // Tiles of a segment of `rows` rows in the main table (the rule both tile-table builders
 // follow), and whether its remainder takes a light tile instead.
+// A remainder (rows past the segment's full tiles) is folded into the last full tile when it
+// holds at most fold rows (and there is a full tile), else it takes a light tile when it holds
+// at most light rows, else a tile of its own.
+__host__ __device__ inline bool seg_folds(int rows, int tile_rows, int fold) {
+    const int n = rows / tile_rows, rem = rows - n * tile_rows;
+    return rem > 0 && n > 0 && rem <= fold;
+}
+__host__ __device__ inline int seg_light(int rows, int tile_rows, int fold, int light) {
+    const int rem = rows % tile_rows;
+    return (rem > 0 && rem <= light && !seg_folds(rows, tile_rows, fold)) ? 1 : 0;
+}
 __host__ __device__ inline int seg_tiles(int rows, int tile_rows, int fold, int light = 0) {
     const int n = rows / tile_rows, rem = rows - n * tile_rows;
-    return n + ((rem > 0 && !(n > 0 && rem <= fold) && rem > light) ? 1 : 0);
-}
-__host__ __device__ inline int seg_light(int rows, int tile_rows, int light) {
-    const int rem = rows % tile_rows;
-    return (rem > 0 && rem <= light) ? 1 : 0;
+    return n + ((rem > 0 && !seg_folds(rows, tile_rows, fold) && !seg_light(rows, tile_rows, fold, light)) ? 1 : 0);
 }
 
-// Rows of a light tile: the weight-streaming form's 32-row tile (cfg5 FFN, one box: 256-row
-// tiles only 7.62-7.65 ms; light tiles of 16, 32, 64 rows 7.45-7.50, 7.19-7.21, 7.37 ms).
-constexpr int kLightRows = 32;
-
-// Whether the LDS-tiled expert GEMMs send remainders of at most kLightRows rows to the
-// weight-streaming form: when experts hold few tiles each (a mean under two 256-row tiles) and
-// remainders are not folded. A 256-row tile that holds a few dozen rows still streams and
-// dequantizes the expert's weights through LDS, at about half the cost of a full tile; the
-// streaming form reads them once from HBM with no LDS round trip for the weights.
+// Whether, and up to how many rows, the LDS-tiled expert GEMMs send remainders to the
+// weight-streaming form (light tiles of 32 or 64 rows, the light value): when experts hold few
+// tiles each (a mean under two 256-row tiles). A 256-row tile that holds a few dozen rows still
+// streams and dequantizes the expert's weights through LDS, at about half the cost of a full
+// tile; the streaming form reads them once from HBM with no LDS round trip for the weights.
+// Without folding: remainders of at most 32 rows (cfg5 FFN, one box: 256-row tiles only
+// 7.62-7.65 ms; light tiles of 16, 32, 64 rows 7.45-7.50, 7.19-7.21, 7.37 ms). With folding
+// (remainders of at most kTileFold rows join their last full tile): the remainders of
+// kTileFold + 1 .. 64 rows.
 inline int tile_light(int N, int k, int E, int fold) {
     const long long mean = (long long)N * k / (E > 0 ? E : 1);
-    return (fold == 0 && mean < 512) ? kLightRows : 0;
+    if (mean >= 512) return 0;
+    return fold > 0 ? 64 : 32;
 }
 
 // Whether the LDS-tiled expert GEMMs fold remainders: when the mean expert holds one tile and

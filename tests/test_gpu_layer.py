@@ -142,16 +142,18 @@ def test_bf16_tiled_prefill_shapes(cuda, oracle):
 @pytest.mark.parametrize("fmt,hidden", [("int8", 256), ("int4", 256), ("fp8", 256), ("bf16", 256),
                                         ("int4", 6144)])
 def test_tiled_folded_remainders(cuda, oracle, fmt, hidden):
-    """Expert segments of 256, 257, 272, 273, 288, 289, 544 and 145 rows and a shared segment of
-    2324 rows (9 x 256 + 20), forced through one-hot gate rows: the LDS-tiled form folds a
-    remainder of 1 .. 32 rows into the segment's last full tile (a second launch runs those
-    tiles; 17+ rows reach the second wavefront row's block) and keeps 33 rows as a tile of
-    their own. int4 at hidden 6144 takes the gate/up form for K > 5120 (2-stage ring beside the
-    64-group scale table)."""
+    """Expert segments of 256, 257, 272, 273, 288, 289, 320, 321, 544 and 16 rows and a shared
+    segment of 2836 rows (11 x 256 + 20), forced through one-hot gate rows: the LDS-tiled form
+    folds a remainder of 1 .. 32 rows into the segment's last full tile (a second launch runs
+    those tiles; 17+ rows reach the second wavefront row's block), sends remainders of 33 .. 64
+    rows and a segment of 16 rows to the weight-streaming form's 64-row light tiles, and keeps
+    65 rows as a tile of its own. int4 at hidden 6144 takes the gate/up form for K > 5120
+    (2-stage ring beside the 64-group scale table)."""
     from pisceslx_amd import _lib
     from pisceslx_amd.workloads import LayerSpec
-    counts = [256, 257, 272, 273, 288, 289, 544, 145]
+    counts = [256, 257, 272, 273, 288, 289, 320, 321, 544, 16]
     E, H, F, N = len(counts), hidden, 256, sum(counts)
+    assert N == 11 * 256 + 20
     spec = LayerSpec("folds", H, F, E, 1, 1, getattr(_lib, "W_" + fmt.upper()), torch.bfloat16,
                      fixed_shape_mode=True)
     w = make_workload(spec, device="cuda", lengths=[N])
