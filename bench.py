@@ -33,7 +33,7 @@ routing): layer step and grouped FFN, the FFN against both rooflines; cfg5 also 
 realised expert load against the Zipf(1.2) target (KL).
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
-       python bench.py --pmc-probe {cfg2,cfg3,moegate}   (launches only, for counter runs)
+       python bench.py --pmc-probe {cfg2,cfg3,cfg5,moegate}   (launches only, for counter runs)
 """
 import argparse
 import dataclasses
@@ -67,7 +67,7 @@ def parse():
     ap.add_argument("--no-norm", action="store_true", help="skip the MoE input RMSNorm timing")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip cfg1 / cfg4 / cfg5 (layer step and FFN against both rooflines)")
-    ap.add_argument("--pmc-probe", choices=["cfg2", "cfg3", "moegate"], default=None,
+    ap.add_argument("--pmc-probe", choices=["cfg2", "cfg3", "cfg5", "moegate"], default=None,
                     help="run the calibration copy and 5 expert-FFN launches (moegate: 3 YvMoEGate "
                          "prefill gate calls), nothing timed")
     return ap.parse_args()
