@@ -144,19 +144,43 @@ def head_logits(x: torch.Tensor, p: MoEGateParams) -> Dict[str, torch.Tensor]:
     """The pieces of step 2 (float64), before the weights w_*."""
     hicl = dg_sparse(x, p) @ p.prototypes.t()
     got = x @ p.got_proj.t()
-    lk, lv = x @ p.gate_k.t(), x @ p.gate_v.t()
-    sw = torch.sigmoid((lk - lower_median(lk)[:, None]) / p.soft_temperature)
-    soft = sw * torch.softmax(lv, dim=-1)
-    soft = soft / soft.sum(dim=-1, keepdim=True).clamp(min=p.eps)
+    soft = soft_weights(x, p)
     ie = F.silu(x @ p.enc0.t()) @ p.enc2.t()
     ee = F.silu(p.expert_embeddings @ p.cap0.t()) @ p.cap2.t()
     return {"gate": x @ p.gate.t(), "hicl": hicl, "got": got, "soft": soft, "eo": ie @ ee.t()}
 
 
+def gate_loss(logits: torch.Tensor, soft: Optional[torch.Tensor], p: MoEGateParams) -> float:
+    """The eval loss (gate.py:433-444, :556-610) of a batch's final logits [N, E] (float64)
+    and, with the SoftMoE head on, its SoftMoE weights [N, E]: load balance over the mean
+    scores plus the capacity term, z-loss, SoftMoE budget."""
+    E = logits.shape[-1]
+    scores = torch.softmax(logits, dim=-1)
+    lb = p.load_balance_alpha * torch.sum((scores.mean(dim=0) - 1.0 / E) ** 2)
+    if p.total_routing_count > 0:
+        usage = p.usage_count / p.total_routing_count
+        lb = lb + 0.005 * torch.sum(torch.relu(usage - p.capacity_limit) ** 2)
+    z = p.z_loss_alpha * torch.mean(logits ** 2)
+    budget = 0.0
+    if "soft_moe" in p.heads:
+        budget = 0.01 * (soft.sum(dim=-1).mean() - p.soft_budget) ** 2
+    return float(lb + z + budget)
+
+
+def soft_weights(x: torch.Tensor, p: MoEGateParams) -> torch.Tensor:
+    """SoftMoE weights [N, E] of x [N, H] (float64), as head_logits computes them."""
+    lk, lv = x @ p.gate_k.t(), x @ p.gate_v.t()
+    sw = torch.sigmoid((lk - lower_median(lk)[:, None]) / p.soft_temperature)
+    soft = sw * torch.softmax(lv, dim=-1)
+    return soft / soft.sum(dim=-1, keepdim=True).clamp(min=p.eps)
+
+
 def moegate_forward(x3d: torch.Tensor, p: MoEGateParams, k: int,
-                    modal_id: Optional[torch.Tensor] = None) -> Dict[str, object]:
+                    modal_id: Optional[torch.Tensor] = None,
+                    seq_len: Optional[int] = None) -> Dict[str, object]:
     """Eval forward of x [B, S, H]: final logits (float64), scores, top-k weights / indices
-    (from the float64 scores), and the loss terms."""
+    (from the float64 scores), and the loss terms. ``seq_len`` overrides S in the temperature
+    rule (x then holds sampled tokens of longer sequences; the loss is over the given tokens)."""
     B, S, H = x3d.shape
     x = x3d.reshape(-1, H).double()
     E = p.gate.shape[0]
@@ -172,19 +196,12 @@ def moegate_forward(x3d: torch.Tensor, p: MoEGateParams, k: int,
             m = m.reshape(B, 1).expand(B, S) if m.numel() == B else m.reshape(B, S)
         logits = logits + p.modal_affinity[:, m.reshape(-1).long()].t()
     logits = logits + p.expert_bias
-    eff = effective_temperature(p.temperature, p.temperature_max, S, p.temp_dtype)
+    eff = effective_temperature(p.temperature, p.temperature_max, S if seq_len is None else seq_len,
+                                p.temp_dtype)
     logits = logits / eff
     scores = torch.softmax(logits, dim=-1)
     kk = min(k, E)
     ts, idx = topk_lower_index(scores, kk)
     w = torch.softmax(ts, dim=-1)
-    lb = p.load_balance_alpha * torch.sum((scores.mean(dim=0) - 1.0 / E) ** 2)
-    if p.total_routing_count > 0:
-        usage = p.usage_count / p.total_routing_count
-        lb = lb + 0.005 * torch.sum(torch.relu(usage - p.capacity_limit) ** 2)
-    z = p.z_loss_alpha * torch.mean(logits ** 2)
-    budget = 0.0
-    if "soft_moe" in p.heads:
-        budget = 0.01 * (h["soft"].sum(dim=-1).mean() - p.soft_budget) ** 2
     return {"logits": logits, "scores": scores, "weights": w, "indices": idx,
-            "loss": float(lb + z + budget), "heads": h, "temperature": eff}
+            "loss": gate_loss(logits, h["soft"], p), "heads": h, "temperature": eff}

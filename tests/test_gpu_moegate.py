@@ -9,7 +9,7 @@ oracle's. Cases: the decode shape of the 7B-style layer (hidden 4096, 64 experts
 ties at the 32nd DG activation, more candidates than the ranking takes (exact radix
 select), fewer than 32 positive DG activations, modal ids, a pruned
 head, the long-sequence temperature, fp32 activations, N = 0, determinism, and the PathMoE
-stage cache.
+stage cache; and the bench's 16,721-token prefill shape at full size on sampled tokens.
 """
 import numpy as np
 import pytest
@@ -232,3 +232,41 @@ def test_moegate_wave_form_dg_selection_cases(cuda, oracle):
         b[[700, 5, 1000, 11, 400]] = 3.5
         dg.dg_bias.copy_(b)
     _check(g, x, oracle)
+
+
+def test_moegate_full_size_prefill_sampled_tokens(cuda, oracle):
+    """The bench's prefill gate shape at full size: one sequence of 16,721 tokens, hidden 4096,
+    64 experts, top-6, every head weighted 1 (the wide projection over 66 row tiles, the
+    wavefront-per-token selection over 1,024 work-groups, the loss over their sums, the long-
+    sequence temperature). Checked: the logits of 64 sampled tokens against the float64 oracle
+    (temperature rule at the full sequence length), the routing of every token bit for bit
+    against the C oracle given the GPU's logits, and the loss against the oracle's loss formula
+    over every token's GPU logits and float64 SoftMoE weights."""
+    from oracle import moegate_oracle as mgo
+    H, E, k, N = 4096, 64, 6, 16721
+    g = _gate(H, E, k, scale_heads=True, seed=11)
+    x = torch.randn(1, N, H, generator=torch.Generator().manual_seed(12)).to(torch.bfloat16)
+    print(f"moegate full size N={N} H={H} E={E} k={k}", flush=True)
+    scores, idx, loss = g(x.cuda())
+    torch.cuda.synchronize()
+    lg = g.last_logits.cpu()
+    p = mgo.params_from_state_dict(g.state_dict(), g.gate.weight.dtype,
+                                   soft_temperature=g.soft_moe_temperature)
+    tokens = np.sort(np.random.default_rng(13).choice(N, 64, replace=False))
+    o = mgo.moegate_forward(x[0, tokens][None], p, k, seq_len=N)
+    assert o["temperature"] == 0.8984375  # bf16(3.0 * 0.3): the long-sequence rule applied
+    ref = o["logits"].numpy()
+    got = lg[tokens].numpy()
+    tol = 1e-4 * max(1.0, float(np.abs(ref).max()))
+    err = float(np.abs(got - ref).max())
+    print(f"  sampled logits max_abs={err:.3e} (tol {tol:.1e})", flush=True)
+    assert err <= tol
+    r = oracle.route(lg.numpy().astype(np.float32), k, -1, None)
+    routing = g.last_routing
+    assert np.array_equal(idx.cpu().numpy(), r.indices.astype(np.int64))
+    assert np.array_equal(routing.weights.cpu().numpy().view(np.uint32), r.weights.view(np.uint32))
+    assert np.array_equal(routing.counts.cpu().numpy(), r.counts)
+    assert np.array_equal(routing.perm.cpu().numpy(), r.perm)
+    want_loss = mgo.gate_loss(lg.double(), mgo.soft_weights(x[0].double(), p), p)
+    print(f"  loss {float(g._last_loss_f32):.6e} oracle formula {want_loss:.6e}", flush=True)
+    assert float(g._last_loss_f32) == pytest.approx(want_loss, rel=1e-4, abs=1e-7)
