@@ -1960,14 +1960,17 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     }
     const int wf = w->format;
     // the light table's remainders (at most tt.light rows, one per segment) on the streaming
-    // form with tt.light-row tiles, after the main table's launch of the same GEMM
+    // form with tt.light-row tiles, after the main table's launch of the same GEMM; 32-row
+    // tiles with four 16-column blocks per wavefront (a quarter of the activation staging per
+    // weight byte: cfg5 FFN -1.9 % against one block), 64-row tiles with one (1, 2 and 4
+    // blocks measured alike at cfg4)
     auto light_launch = [&](GemmParams q, auto epi, const char* name) {
         constexpr int EPIV = decltype(epi)::value;
         q.tile_seg = tt.ltile_seg;
         q.tile_row0 = tt.ltile_row0;
         q.ntiles = tt.lntiles;
         if (tt.light > 32) return stream_dispatch<EPIV, 2, 1, 4, true, 4>(wf, q, E + S, st, name);
-        return stream_dispatch<EPIV, 2, 1, 2, true, 4>(wf, q, E + S, st, name);
+        return stream_dispatch<EPIV, 2, 4, 2, true, 4>(wf, q, E + S, st, name);
     };
     GemmParams p{};
     p.tile_seg = tile_seg;
