@@ -1852,7 +1852,11 @@ int dense_partials_launch(const void* x, int act, int N, int K, const void* w, i
     if (dense_tiled(act, N, ncols, K)) return tile_dispatch<EPI_F32>(YVMOE_W_BF16, p, ceil_div(N, TBM), st, name);
     if (dense_streamed(act, N, ncols, K)) {
         if (N <= 16) return stream_dispatch<EPI_F32, 4, 1, 1>(YVMOE_W_BF16, p, 1, st, name, ks);
-        return stream_dispatch<EPI_F32, 2, 1, 4, YV_DPF>(YVMOE_W_BF16, p, 1, st, name, ks);
+        // one k-step per staged chunk with the next chunk's weights in flight: the YvMoEGate
+        // decode projection (64 x 4096 x 16,896) 35.1-35.7 -> 33.0-33.6 us against two k-steps
+        // (4/8/16 wavefronts, 1-4 column blocks per wavefront and 1-16 K splits measured slower
+        // or needing more partial sums)
+        return stream_dispatch<EPI_F32, 1, 1, 4, YV_DPF>(YVMOE_W_BF16, p, 1, st, name, ks);
     }
     const int wf = (act == YVMOE_ACT_F32) ? YVMOE_W_F32 : YVMOE_W_BF16;
     return gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), (ncols % 32 == 0) ? 2 : 1, ks,
