@@ -256,7 +256,7 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
  * called) and held until the process ends: every process that uses the library pays 64 MiB
  * of device memory per GPU it runs on. A call whose yvmoe_workspace_bytes() exceeds it
  * returns YVMOE_ERR_WORKSPACE (at cfg2's shape, hidden 4096 / 64 experts / top-6 / 2 shared,
- * up to 689 tokens fit). Every call on one GPU shares that GPU's scratch, which keeps the last
+ * up to 635 tokens fit). Every call on one GPU shares that GPU's scratch, which keeps the last
  * call's contents: calls that overlap on one GPU (other streams, other host threads) race.
  */
 #define YVMOE_STATIC_SCRATCH_BYTES (64u << 20)

@@ -873,20 +873,26 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     // grouped: tiles from the tile table; dense (no table): 256-row tiles of nrows rows
     const bool dense = p.tile_seg == nullptr;
     const int ntl = dense ? (p.nrows + TBM - 1) / TBM : *p.ntiles;
-    const int total = ntl * ncb;
+    // fp32 output: the items also run over K splits (split kz: K range kz * kchunk .. + kchunk,
+    // the last one shorter), column block fastest, then split, then tile
+    const int nsplit = EPI == EPI_F32 ? (p.K + p.kchunk - 1) / p.kchunk : 1;
+    const int total = ntl * ncb * nsplit;
     const int per_xcd = (total + 7) / 8;
     const int local = blockIdx.x / 8;
     if (local >= per_xcd) return;
     const int item = (blockIdx.x % 8) * per_xcd + local;
     if (item >= total) return;
-    const int tile = item / ncb;
+    const int tile = item / (ncb * nsplit);
+    const int kz = EPI == EPI_F32 ? (item / ncb) % nsplit : 0;
     const int cb = item % ncb;
     const int e = dense ? 0 : p.tile_seg[tile];
     const int row0 = dense ? tile * TBM : p.tile_row0[tile];
     const int seg_end = dense ? p.nrows : p.seg_start[e + 1];
-    // output columns: gate/up -> 128 columns (x2 matrices); down -> 256 columns
+    // output columns: gate/up -> 128 columns (x2 matrices); down -> 256 columns (fp32 output:
+    // the last column block may end early, at ncols, a multiple of 16)
     const int n0 = SWIGLU ? cb * (TBN / 2) : cb * TBN;
-    const int nks = p.K / TBK;
+    const int kbeg = EPI == EPI_F32 ? kz * p.kchunk : 0;
+    const int nks = EPI == EPI_F32 ? (min(p.K, kbeg + p.kchunk) - kbeg) / TBK : p.K / TBK;
     const long long e_off = (long long)e * p.b_stride;
     const long long s_off = (long long)e * p.s_stride;
 
@@ -906,7 +912,7 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
             const int r = blk * 8 + lane / 8;
             const int lc = (lane % 8) ^ (lane / 8) ^ (blk & 1);
             const int gr = (row0 + r < seg_end) ? row0 + r : row0;
-            a_src[j] = (const char*)p.A + ((long long)map_row(p, gr) * p.lda + lc * 8) * 2;
+            a_src[j] = (const char*)p.A + ((long long)map_row(p, gr) * p.lda + kbeg + lc * 8) * 2;
         }
         // folded rows: wavefront w loads rows 256 + 2 w and + 1, lane L dword L % 4 of physical
         // chunk (L % 32) / 4 of row 256 + 2 w + L / 32 (the same swizzle as the other rows)
@@ -929,9 +935,13 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
             const int half = C::I4 ? j : blk % C::EB;
             const int r16 = rb * 16;
             const void* B = (SWIGLU && r16 >= TBN / 2) ? p.B1 : p.B0;
-            const int nb16 = SWIGLU ? n0 + (r16 & (TBN / 2 - 1)) : n0 + r16;
+            int nb16 = SWIGLU ? n0 + (r16 & (TBN / 2 - 1)) : n0 + r16;
+            // fp32 output: blocks past ncols load the last block (their wavefront skips its
+            // MFMAs and stores nothing)
+            if (EPI == EPI_F32 && nb16 >= p.ncols) nb16 = p.ncols - 16;
             const long long e_bytes = C::I4 ? e_off / 2 : e_off * C::EB;
             b_src[j] = (const char*)B + e_bytes + (long long)(nb16 >> 4) * (p.K / 64) * B_CHUNK +
+                       (long long)(kbeg / TBK) * B_CHUNK +
                        (C::I4 ? half * 256 + lane * 4 : half * 1024 + lane * 16);
             b_dst[j] = C::I4 ? rb * 512 + half * 256 : blk * 1024;
         }
@@ -1023,6 +1033,9 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
         // 16-row blocks of this wavefront's 128 rows that hold rows of the segment: an expert's
         // last tile skips the MFMAs of the blocks past its end (loads and barriers stay uniform)
         const int live_mb = min(8, max(0, (seg_end - (row0 + wr * 128) + 15) / 16));
+        // fp32 output: a wavefront whose 32 columns lie past ncols skips every MFMA (a separate
+        // flag: folding it into live_mb made the compiler spill 59 VGPRs of this kernel)
+        const bool colive = EPI != EPI_F32 || n0 + wc * 32 < p.ncols;
         // folded rows: wavefront row wr computes row block 256 + 16 wr .. + 15 when it holds rows
         const bool xlive = XT && ext > 16 * wr;
         f32x4 accx[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
@@ -1111,8 +1124,8 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
                 }
             };
             if (xlive) compute(std::false_type{}, std::true_type{});
-            else if (live_mb == 8) compute(std::false_type{}, std::false_type{});
-            else if (live_mb > 0) compute(std::true_type{}, std::false_type{});
+            else if (live_mb == 8 && colive) compute(std::false_type{}, std::false_type{});
+            else if (live_mb > 0 && colive) compute(std::true_type{}, std::false_type{});
             if (++st == C::NST) st = 0;
         }
 #undef YV_TILE_ISSUE
@@ -1137,9 +1150,11 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
                         for (int nb = 0; nb < 2; ++nb) {
                             const int n = n0 + wc * 32 + nb * 16 + (lane & 15);
                             const float v = nb ? c1[i] : c0[i];
-                            if constexpr (EPI == EPI_F32)
-                                ((float*)p.out)[(long long)r * p.ldo + n] = f32_out(p, v, n, 0);
-                            else
+                            if constexpr (EPI == EPI_F32) {
+                                if (n < p.ncols)
+                                    ((float*)p.out)[kz * p.split_stride + (long long)r * p.ldo + n] =
+                                        f32_out(p, v, n, kz);
+                            } else
                                 ((unsigned short*)p.out)[(long long)r * p.ldo + n] = f32_to_bf16_rne(v);
                         }
                     }
@@ -1661,6 +1676,37 @@ __global__ __launch_bounds__(256) void reduce_splits_kernel(const float* __restr
     for (int z = 1; z < nsplit; ++z) s = s + part[(long long)z * stride + i];
     out[i] = s;
 }
+// The same over four consecutive elements per thread (n and stride multiples of 4, 16-byte
+// aligned arrays): each element sums its splits in the same order.
+__global__ __launch_bounds__(256) void reduce_splits4_kernel(const float4* __restrict__ part, int nsplit,
+                                                             long long stride4, long long n4,
+                                                             float4* __restrict__ out) {
+    const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    float4 s = part[i];
+    for (int z = 1; z < nsplit; ++z) {
+        const float4 v = part[(long long)z * stride4 + i];
+        s.x = s.x + v.x;
+        s.y = s.y + v.y;
+        s.z = s.z + v.z;
+        s.w = s.w + v.w;
+    }
+    out[i] = s;
+}
+// out[i] = sum over z of part[z * n + i], z in order, for i < n.
+int reduce_splits_launch(const float* part, int nsplit, long long n, float* out, hipStream_t st,
+                         const char* name) {
+    if (n <= 0) return YVMOE_OK;
+    if (n % 4 == 0 && ((uintptr_t)part | (uintptr_t)out) % 16 == 0) {
+        const long long n4 = n / 4;
+        reduce_splits4_kernel<<<(unsigned)((n4 + 255) / 256), 256, 0, st>>>(
+            (const float4*)part, nsplit, n4, n4, (float4*)out);
+    } else {
+        reduce_splits_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(part, nsplit, n, n, out);
+    }
+    YV_LAUNCH_CHECK(name);
+    return YVMOE_OK;
+}
 
 // Streaming (decode) form: one (tile, column group) item per work-group; NB 16-column
 // blocks per wavefront.
@@ -1710,21 +1756,28 @@ int tile_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, c
 template <int EPI, bool FOLD>
 int tile_launch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, const char* name) {
     const int cols = (EPI == EPI_SWIGLU) ? TBN / 2 : TBN;
-    if (p.ncols % cols != 0 || p.K % TBK != 0) {
-        set_error("%s: tiled form needs columns %% %d == 0 and K %% %d == 0", name, cols, TBK);
+    // the fp32-output form takes any multiple of 16 columns (a partial last column block) and
+    // K splits of kchunk (a multiple of 64; the last split may be shorter)
+    const int cmul = EPI == EPI_F32 ? 16 : cols;
+    if (p.ncols % cmul != 0 || p.K % TBK != 0 || (EPI == EPI_F32 && (p.kchunk <= 0 || p.kchunk % TBK != 0))) {
+        set_error("%s: tiled form needs columns %% %d == 0 and K %% %d == 0 (K=%d, kchunk=%d)", name,
+                  cmul, TBK, p.K, p.kchunk);
         return YVMOE_ERR_SHAPE;
     }
     if (ntiles_max <= 0) return YVMOE_OK;
-    const int ncb = p.ncols / cols;
-    const long long blocks = 8LL * ceil_div(ntiles_max * ncb, 8);
+    const int ncb = ceil_div(p.ncols, cols);
+    const int nsplit = EPI == EPI_F32 ? ceil_div(p.K, p.kchunk) : 1;
+    const long long blocks = 8LL * ceil_div(ntiles_max * ncb * nsplit, 8);
     if (EPI == EPI_F32 && (p.tile_seg != nullptr || wf != YVMOE_W_BF16)) {
         set_error("%s: the fp32-output tiled form is dense with bf16 weights", name);
         return YVMOE_ERR_UNSUPPORTED;
     }
     if constexpr (EPI == EPI_F32) {
-        // a grid that fills the chip (and whose activation offsets fit 31 bits) takes the wide
-        // four-wavefront form; fewer tiles (the router GEMM) keep 16 wavefronts per CU
-        if (ntiles_max * ncb >= 256 && (long long)p.nrows * p.lda * 2 < (1ll << 31) && p.kchunk == p.K)
+        // a grid that fills the chip with whole column blocks and no K split (and whose
+        // activation offsets fit 31 bits) takes the wide four-wavefront form; fewer tiles (the
+        // router GEMM) keep 16 wavefronts per CU
+        if (ntiles_max * ncb >= 256 && (long long)p.nrows * p.lda * 2 < (1ll << 31) && nsplit == 1 &&
+            p.ncols % TBN == 0)
             gemm_wide_kernel<<<(unsigned)blocks, 256, 0, st>>>(p, ncb);
         else
             gemm_tile_kernel<YVMOE_W_BF16, EPI><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb);
@@ -1824,10 +1877,7 @@ int dense_gemm_launch(const void* x, int act, int N, int K, const void* w, int n
     p.split_stride = (long long)N * ld;
     int rc = gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), ncb, ks, st, name);
     if (rc) return rc;
-    const long long n = (long long)N * ld;
-    reduce_splits_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(partials, ks, n, n, out);
-    YV_LAUNCH_CHECK("dense_gemm_reduce");
-    return YVMOE_OK;
+    return reduce_splits_launch(partials, ks, (long long)N * ld, out, st, "dense_gemm_reduce");
 }
 
 int dense_partials_launch(const void* x, int act, int N, int K, const void* w, int ncols,
@@ -1875,14 +1925,22 @@ int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, flo
     p.ldo = ld;
     p.nrows = N;
     const int wf = (act == YVMOE_ACT_F32) ? YVMOE_W_F32 : YVMOE_W_BF16;
-    if (N > kSmallRouteTok && dense_tiled(act, N, p.ncols, r->hidden)) {
-        // large batches with a 256-multiple operand width (E <= 64 with bf16 activations):
-        // the LDS-tiled MFMA form, no K split
-        p.kchunk = r->hidden;
-        p.out = out;
-        return tile_dispatch<EPI_F32>(YVMOE_W_BF16, p, ceil_div(N, TBM), st, "router_gemm");
-    }
     const int ks = router_ksplit(N, r->num_experts, act, r->hidden);
+    if (router_tiled(act, N, p.ncols, r->hidden)) {
+        // large batches: the LDS-tiled MFMA form over (tile, column block, K split) items, the
+        // split partial sums reduced in split order
+        if (ks == 1 || partials == nullptr) {
+            p.kchunk = r->hidden;
+            p.out = out;
+            return tile_dispatch<EPI_F32>(YVMOE_W_BF16, p, ceil_div(N, TBM), st, "router_gemm");
+        }
+        p.kchunk = router_tiled_steps(N, p.ncols, r->hidden) * 64;
+        p.out = partials;
+        p.split_stride = (long long)N * ld;
+        int rc = tile_dispatch<EPI_F32>(YVMOE_W_BF16, p, ceil_div(N, TBM), st, "router_gemm");
+        if (rc || !reduce) return rc;
+        return reduce_splits_launch(partials, ks, (long long)N * ld, out, st, "router_reduce");
+    }
     p.kchunk = r->hidden / ks;
     if (ks == 1 || partials == nullptr) {
         p.kchunk = r->hidden;
@@ -1901,10 +1959,7 @@ int router_gemm_launch(const void* x, int act, int N, const yvmoe_router* r, flo
     else
         rc = gemm_dispatch<EPI_F32>(act, wf, p, ceil_div(N, kTileRows), 1, ks, st, "router_gemm");
     if (rc || !reduce) return rc;
-    const long long n = (long long)N * ld;
-    reduce_splits_kernel<<<(unsigned)((n + 255) / 256), 256, 0, st>>>(partials, ks, n, n, out);
-    YV_LAUNCH_CHECK("router_reduce");
-    return YVMOE_OK;
+    return reduce_splits_launch(partials, ks, (long long)N * ld, out, st, "router_reduce");
 }
 
 int ffn_tile_rows(int act, int N, int k, int E, int H, int F, int wf) {

@@ -57,7 +57,38 @@ constexpr int kSmallRouteTok = 256;
 #define YV_ROUTER_KS_MAX 16
 #endif
 
+// Router GEMMs of more than kSmallRouteTok tokens with bf16 operands run on the LDS-tiled MFMA
+// form: 256 x 256 output tiles (the last column block may be partial), K split so that the
+// (tile, column block, split) items spread over the 256 CUs.
+inline bool router_tiled(int act, int N, int ncols, int K) {
+    return act == YVMOE_ACT_BF16 && N > kSmallRouteTok && ncols % 16 == 0 && K % 64 == 0 && K > 0;
+}
+
+// k-steps (of 64) per split of the tiled router GEMM: the choice with the least estimated time,
+// counted in tile k-steps: rounds of 256 items (one work-group per CU) times k-steps per split,
+// plus, when split, the partial sums' extra HBM traffic (ks arrays of N x ncols fp32 written
+// by the GEMM and read back by the reduction) at 8 MB per k-step. At most 16 splits.
+inline int router_tiled_steps(int N, int ncols, int K) {
+    const int units = ceil_div(N, 256) * ceil_div(ncols, 256);
+    const int nks = K / 64;
+    const double arr = (double)N * ncols * 4 / 8.0e6;
+    int best = nks;
+    double best_t = (double)ceil_div(units, 256) * nks;
+    for (int steps = nks - 1; steps >= 1; --steps) {
+        const int ks = ceil_div(nks, steps);
+        if (ks > 16) break;
+        const double t = (double)ceil_div(units * ks, 256) * steps + 2.0 * ks * arr;
+        if (t < best_t) {
+            best = steps;
+            best_t = t;
+        }
+    }
+    return best;
+}
+
 inline int router_ksplit(int N, int E, int act, int H) {
+    const int ld = router_ld(E, act);
+    if (router_tiled(act, N, ld, H)) return ceil_div(H / 64, router_tiled_steps(N, ld, H));
     const int groups = ceil_div(router_ld(E, act), 64);
     const int wgs = ceil_div(N > 0 ? N : 1, 64) * groups;
     int ks = 1;

@@ -42,6 +42,22 @@ def test_workspace_bytes_is_host_only():
     assert big >= 16384 * 8 * (4096 + 1408) * 2
 
 
+@pytest.mark.parametrize("N,H,E,splits", [
+    (16721, 4096, 64, 3),   # cfg3 prefill: 66 tiles x 3 splits = 198 work-groups, one round
+    (8192, 7168, 256, 4),   # cfg5: 32 tiles x 2 column blocks x 4 splits = 256
+    (4344, 5120, 128, 7),   # cfg4: 17 x 2 x 7 = 238 (splits of 12 k-steps, the last 8)
+    (512, 4096, 64, 16),    # 2 tiles: the most splits
+    (64, 4096, 64, 16),     # decode: the streaming form's 16 splits
+])
+def test_router_split_partials(N, H, E, splits):
+    """The router GEMM's K splits, seen through the partial-sum workspace it asks for: one
+    fp32 [N][Ep + 192] array per split (none without a split)."""
+    r = _lib.Router(E, H, 6, 0, 0, 4, 1.0, None, None, None, None, None)
+    ld = (E + 15) // 16 * 16 + 3 * _lib.PREDICTOR_DIM
+    want = -(-(splits * N * ld * 4) // 256) * 256
+    assert _lib.lib().yvmoe_router_workspace_bytes(N, _lib.ACT_BF16, ctypes.byref(r)) == want
+
+
 @pytest.mark.parametrize("E,k,code", [(0, 1, _lib.YVMOE_ERR_SHAPE), (257, 2, _lib.YVMOE_ERR_SHAPE),
                                       (8, 9, _lib.YVMOE_ERR_SHAPE), (8, 0, _lib.YVMOE_ERR_SHAPE),
                                       (64, 17, _lib.YVMOE_ERR_SHAPE)])
