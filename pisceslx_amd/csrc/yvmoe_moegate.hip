@@ -82,6 +82,27 @@ __device__ __forceinline__ float wave_max(float v) {
     v = fmaxf(v, ror16<1>(v));
     return fmaxf(fmaxf(lane_of(v, 0), lane_of(v, 16)), fmaxf(lane_of(v, 32), lane_of(v, 48)));
 }
+// The m-th smallest (0-based, counted with multiplicity) of the keys of the wavefront's lanes
+// that have `valid` set, in every lane: bisection from the top bit, each step one compare, one
+// ballot and a population count (scalar) instead of a rank loop over the lanes.
+__device__ __forceinline__ unsigned wave_kth_smallest(unsigned key, bool valid, unsigned m) {
+    unsigned ans = 0u;
+#pragma unroll
+    for (int b = 31; b >= 0; --b) {
+        const unsigned test = ans | (1u << b);
+        if ((unsigned)__popcll(__ballot(valid && key < test)) <= m) ans = test;
+    }
+    return ans;
+}
+// fp32 bit patterns mapped to unsigned keys that order like the values (-0 just below +0).
+__device__ __forceinline__ unsigned f32_order_key(float x) {
+    const unsigned b = __float_as_uint(x);
+    return (b >> 31) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float f32_from_order_key(unsigned k) {
+    return __uint_as_float((k >> 31) ? (k & 0x7fffffffu) : ~k);
+}
+
 // Maximum over each row of 16 lanes.
 __device__ __forceinline__ float row_max(float v) {
     v = fmaxf(v, ror16<8>(v));
@@ -293,6 +314,9 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
     __shared__ unsigned ctl[8];
     __shared__ float s_med, s_tlb;
     __shared__ float s_rl[64];  // the token's logits for its top-k (do_topk)
+    __shared__ int s_rank[64];  // candidate ranks (at most 64 candidates)
+    __shared__ float s_lv[64];    // gate_v of the token's experts (E <= 64)
+    __shared__ float s_soft[65];  // SoftMoE weights of the token's experts, their sum (E <= 64)
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int E = a.E, D = a.D, K = a.sel_k;
     const bool is_e = tid < E;
@@ -368,6 +392,7 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
             }
         }
         if (is_e) s_lk[tid] = lk;
+        if (is_e && E <= 64) s_lv[tid] = lv;
         if (eo_on && tid < D) s_h[tid] = h1 / (1.f + expf(-h1));  // SiLU
         float modal_e = 0.f;  // affinity of this token's modality (gate.py:369-376)
         if (is_e && a.modal_id != nullptr) {
@@ -400,19 +425,18 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
             if ((lane & 15) == 0) gmax[tid >> 4] = m;
             __syncthreads();
             if (wave == 0) {
-                const float mv = lane < NGRP ? gmax[lane] : 0.f;
-                const int mvb = __float_as_int(mv);
-                unsigned r = 0u;
-#pragma unroll 8
-                for (int k = 0; k < NGRP; ++k) {
-                    const float g = __int_as_float(__builtin_amdgcn_readlane(mvb, k));
-                    r += (g > mv || (g == mv && k < lane)) ? 1u : 0u;
+                // the sel_k-th largest group maximum = the (NGRP - sel_k)-th smallest (the maxima
+                // are non-negative: their bit patterns order like the values)
+                const unsigned mv = lane < NGRP ? __float_as_uint(gmax[lane]) : 0u;
+                const unsigned th = wave_kth_smallest(mv, lane < NGRP, (unsigned)(NGRP - K));
+                if (lane == 0) {
+                    s_tlb = __uint_as_float(th);
+                    ctl[5] = 0u;
                 }
-                if (lane < NGRP && r == (unsigned)(K - 1)) s_tlb = mv;
-                if (lane == 0) ctl[5] = 0u;
             }
             __syncthreads();
             const unsigned tlb = __float_as_uint(s_tlb);
+            if (tid < 64) s_rank[tid] = 0;  // read after the barriers below
             // 2. candidates
 #pragma unroll
             for (int j = 0; j < JV; ++j) {
@@ -456,19 +480,24 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
 #undef IDX
             // 3. rank order (value descending, index ascending); ranks below K are kept
             if (C <= 64) {
-                if (wave == 0) {
-                    const bool in = lane < C;
-                    const unsigned mv = in ? __float_as_uint(cand_val[lane]) : 0u;
-                    const int mi = in ? cand_idx[lane] : 0;
-                    int r = 0;
-                    for (int k = 0; k < C; ++k) {
-                        const unsigned cv = (unsigned)__builtin_amdgcn_readlane((int)mv, k);
-                        const int ci = __builtin_amdgcn_readlane(mi, k);
-                        r += (cv > mv || (cv == mv && ci < mi)) ? 1 : 0;
-                    }
-                    if (in && r < K) {
-                        sel_val[r] = __uint_as_float(mv);
-                        sel_idx[r] = mi;
+                // lane i of every wavefront holds candidate i; wavefront w counts the candidates
+                // k = w, w + NT / 64, ... that rank above it, and the partial ranks add up in LDS
+                const bool in = lane < C;
+                const unsigned mv = in ? __float_as_uint(cand_val[lane]) : 0u;
+                const int mi = in ? cand_idx[lane] : 0;
+                int r = 0;
+                for (int k = wave; k < C; k += NT / 64) {
+                    const unsigned cv = __float_as_uint(cand_val[k]);
+                    const int ci = cand_idx[k];
+                    r += (cv > mv || (cv == mv && ci < mi)) ? 1 : 0;
+                }
+                if (in && r > 0) atomicAdd(&s_rank[lane], r);
+                __syncthreads();
+                if (wave == 0 && in) {
+                    const int rr = s_rank[lane];
+                    if (rr < K) {
+                        sel_val[rr] = __uint_as_float(mv);
+                        sel_idx[rr] = mi;
                     }
                 }
             } else if (tid < C) {
@@ -510,6 +539,25 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
             }
             s_ph[q][o] = h;
         }
+        // SoftMoE of a gate with at most 64 experts (lane e: expert e), by wavefront 1 beside the
+        // HiCL dot products, for wavefront 0's logits after the barrier
+        if (E <= 64 && wave == 1 && (a.mask & YVMOE_HEAD_SOFT)) {
+            const bool ve = lane < E;
+            const float lk1 = ve ? s_lk[lane] : 0.f;
+            const float lv1 = ve ? s_lv[lane] : 0.f;
+            // torch.median: the lower middle value, the ((E - 1) / 2)-th smallest (equal values
+            // have equal bits except +-0, which give the same lk - med)
+            const float med = f32_from_order_key(
+                wave_kth_smallest(f32_order_key(lk1), ve, (unsigned)((E - 1) / 2)));
+            const float mx = wave_max(ve ? lv1 : -INFINITY);
+            const float ex = ve ? expf(lv1 - mx) : 0.f;
+            const float se = wave_sum(ex);
+            float sv = ve ? (1.f / (1.f + expf(-((lk1 - med) / a.soft_t)))) * (ex / se) : 0.f;
+            sv = sv / fmaxf(wave_sum(sv), a.soft_eps);
+            s_soft[lane] = sv;
+            const float tot = wave_sum(sv);
+            if (lane == 0) s_soft[64] = tot;
+        }
         __syncthreads();
         float hicl = 0.f, eo = 0.f;
         if (is_e) {
@@ -533,31 +581,15 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
             if (eo_on) l = l + a.w_eo * eo;
             if (a.modal_id != nullptr) l = l + modal_e;
             if (a.ebias != nullptr) l = l + bias_e;
-            l = l / a.temp;
-            a.logits[(long long)t * E + tt] = l;
-            return l;
+            return l / a.temp;
         };
         if (E <= 64) {
             // one wavefront holds every expert: wave reductions, no barriers
             if (wave == 0) {
                 float soft = 0.f, soft_tot = 0.f;
-                if (a.mask & YVMOE_HEAD_SOFT) {
-                    // torch.median: the lower middle value (rank, ties by index)
-                    const int lkb = __float_as_int(lk);
-                    unsigned r = 0u;
-                    for (int j = 0; j < E; ++j) {
-                        const float x = __int_as_float(__builtin_amdgcn_readlane(lkb, j));
-                        r += (x < lk || (x == lk && j < tid)) ? 1u : 0u;
-                    }
-                    const int ml = __ffsll((long long)__ballot(is_e && r == (unsigned)((E - 1) / 2))) - 1;
-                    const float med = __shfl(lk, ml);
-                    const float mx = wave_max(is_e ? lv : -INFINITY);
-                    const float ex = is_e ? expf(lv - mx) : 0.f;
-                    const float se = wave_sum(ex);
-                    float sv = is_e ? (1.f / (1.f + expf(-((lk - med) / a.soft_t)))) * (ex / se) : 0.f;
-                    sv = sv / fmaxf(wave_sum(sv), a.soft_eps);
-                    soft = sv;
-                    soft_tot = wave_sum(sv);
+                if (a.mask & YVMOE_HEAD_SOFT) {  // from wavefront 1
+                    soft = s_soft[tid];
+                    soft_tot = s_soft[64];
                 }
                 const float l = is_e ? logit(soft) : 0.f;
                 if (a.do_topk) {
@@ -571,6 +603,8 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
                     if (lane < kLanes) token_topk(s_rl, lane, E, a.tk, t);
                     __builtin_amdgcn_wave_barrier();  // s_rl is rewritten by the next token
                 }
+                // stored after the top-k call, which waits for every outstanding memory access
+                if (is_e) a.logits[(long long)t * E + tt] = l;
                 const float lm = wave_max(is_e ? l : -INFINITY);
                 const float le = is_e ? expf(l - lm) : 0.f;
                 const float ls = wave_sum(le);
@@ -602,6 +636,7 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
                 soft = sv;
             }
             const float l = is_e ? logit(soft) : 0.f;
+            if (is_e) a.logits[(long long)t * E + tt] = l;
             float lm, st;
             block_max_sum<NT>(is_e ? l : -INFINITY, soft, red, lm, st);
             soft_tot = st;
