@@ -546,7 +546,7 @@ __global__ __launch_bounds__(NT) void moegate_token_kernel(GateArgs a) {
             const float lk1 = ve ? s_lk[lane] : 0.f;
             const float lv1 = ve ? s_lv[lane] : 0.f;
             // torch.median: the lower middle value, the ((E - 1) / 2)-th smallest (equal values
-            // have equal bits except +-0, which give the same lk - med)
+            // have equal bits except +0 and -0, and either as med gives the same sigmoid below)
             const float med = f32_from_order_key(
                 wave_kth_smallest(f32_order_key(lk1), ve, (unsigned)((E - 1) / 2)));
             const float mx = wave_max(ve ? lv1 : -INFINITY);
