@@ -263,6 +263,9 @@ __global__ __launch_bounds__(256) void route_scatter_kernel(
 // Capacity trim of one expert: LDS radix select of the cap-th largest p (4 passes of 8
 // bits on the fp32 bit pattern, which orders like the value for p >= 0), then keep
 // p > T and the first (cap - #{p > T}) slots with p == T in token order (gate.py:1228-1236).
+// The first kTrimKeys x 256 slots' keys are gathered once (perm, then p) into registers, so
+// the five passes over them read no memory; slots past those are gathered on every pass.
+constexpr int kTrimKeys = 16;
 __global__ __launch_bounds__(256) void capacity_trim_kernel(
     const int* __restrict__ counts, const int* __restrict__ offsets, const int* __restrict__ cap_ptr,
     const int* __restrict__ perm, const float* __restrict__ topp, uint8_t* __restrict__ allowed) {
@@ -282,12 +285,26 @@ __global__ __launch_bounds__(256) void capacity_trim_kernel(
         for (int i = tid; i < n; i += 256) allowed[perm[off + i]] = 0;
         return;
     }
+    // slot i = tid + 256 j of the expert: j < kTrimKeys cached (slot index and key)
+    int cs[kTrimKeys];
+    unsigned ck[kTrimKeys];
+#pragma unroll
+    for (int j = 0; j < kTrimKeys; ++j) {
+        const int i = tid + 256 * j;
+        cs[j] = i < n ? perm[off + i] : -1;
+    }
+#pragma unroll
+    for (int j = 0; j < kTrimKeys; ++j) ck[j] = cs[j] >= 0 ? __float_as_uint(topp[cs[j]]) : 0u;
     unsigned prefix = 0u, pmask = 0u;
     int rem = cap;
     for (int shift = 24; shift >= 0; shift -= 8) {
         hist[tid] = 0u;
         __syncthreads();
-        for (int i = tid; i < n; i += 256) {
+#pragma unroll
+        for (int j = 0; j < kTrimKeys; ++j) {
+            if (cs[j] >= 0 && (ck[j] & pmask) == prefix) atomicAdd(&hist[(ck[j] >> shift) & 255u], 1u);
+        }
+        for (int i = tid + 256 * kTrimKeys; i < n; i += 256) {
             const unsigned key = __float_as_uint(topp[perm[off + i]]);
             if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
         }
@@ -325,12 +342,21 @@ __global__ __launch_bounds__(256) void capacity_trim_kernel(
     }
     const unsigned T = prefix;
     int running = 0;
-    for (int b = 0; b < n; b += 256) {
+    for (int b = 0, j = 0; b < n; b += 256, ++j) {
         const int i = b + tid;
         const bool valid = i < n;
         int slot = -1;
         unsigned key = 0u;
-        if (valid) {
+        if (j < kTrimKeys) {
+            // registers cs / ck by a uniform index: a select chain, no scratch
+#pragma unroll
+            for (int jj = 0; jj < kTrimKeys; ++jj) {
+                if (jj == j) {
+                    slot = cs[jj];
+                    key = ck[jj];
+                }
+            }
+        } else if (valid) {
             slot = perm[off + i];
             key = __float_as_uint(topp[slot]);
         }
