@@ -117,8 +117,15 @@ __global__ __launch_bounds__(1024) void route_scan_kernel(
     if (active) {
         b0 = (int)((long long)c * nb / C);
         b1 = (int)((long long)(c + 1) * nb / C);
+        // eight loads in flight per round trip (a dependent add per load would wait for each)
         int s = 0;
-        for (int b = b0; b < b1; ++b) s += blockhist[(size_t)b * E + e];
+        for (int b = b0; b < b1; b += 8) {
+            int v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[j] = b + j < b1 ? blockhist[(size_t)(b + j) * E + e] : 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) s += v[j];
+        }
         part[c * E + e] = s;
     }
     // fixed-order complexity sum: strided per thread, then a fixed tree
