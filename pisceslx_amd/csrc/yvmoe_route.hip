@@ -56,7 +56,8 @@ __global__ __launch_bounds__(1024) void route_topk_kernel(
     const float* __restrict__ pred, int pred_ld, int pred_terms, const float* __restrict__ b1,
     const float* __restrict__ w2, const float* __restrict__ b2, int N, int E, int k,
     int64_t* __restrict__ idx_out, float* __restrict__ topp, float* __restrict__ w0,
-    uint8_t* __restrict__ allowed, int* __restrict__ blockhist, float* __restrict__ blocksum) {
+    uint8_t* __restrict__ allowed, int* __restrict__ blockhist, float* __restrict__ blocksum,
+    int nsplit, long long sstride) {
     __shared__ int hist[YVMOE_MAX_EXPERTS];
     __shared__ float score[kTokPerBlock];
     const int tid = threadIdx.x;
@@ -71,7 +72,14 @@ __global__ __launch_bounds__(1024) void route_topk_kernel(
     if (t < N) {  // uniform across the 16 lanes of a token
         int my_id;
         float my_ts, my_w0;
-        topk_token<NV>([&](int e) { return logits[(size_t)t * ld + e]; }, bias, l, E, k, my_id, my_ts, my_w0);
+        // the router GEMM's nsplit partial sums (split z at + z * sstride), summed in split order
+        auto split_sum = [&](const float* q) {
+            float v = q[0];
+            for (int z = 1; z < nsplit; ++z) v = v + q[z * sstride];
+            return v;
+        };
+        topk_token<NV>([&](int e) { return split_sum(logits + (size_t)t * ld + e); }, bias, l, E, k, my_id,
+                       my_ts, my_w0);
         if (l < k) {
             const size_t s = (size_t)t * k + l;
             idx_out[s] = (int64_t)my_id;
@@ -81,7 +89,7 @@ __global__ __launch_bounds__(1024) void route_topk_kernel(
             atomicAdd(&hist[my_id], 1);
         }
         if (pred != nullptr) {
-            const float sc = predictor_token([&](int c) { return pred[(size_t)t * pred_ld + c]; },
+            const float sc = predictor_token([&](int c) { return split_sum(pred + (size_t)t * pred_ld + c); },
                                              pred_terms, b1, w2, b2, l);
             if (l == 0) score[tl] = sc;
         }
@@ -873,8 +881,7 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
         route_gate_loss_kernel<<<1, 1024, 0, st>>>(*loss);
         YV_LAUNCH_CHECK("route_gate_loss");
     }
-    YV_REQUIRE(ksplit == 1 && tiles == nullptr, YVMOE_ERR_ARG,
-               "internal: split logits and tile building are for small batches only");
+    YV_REQUIRE(tiles == nullptr, YVMOE_ERR_ARG, "internal: tile building is for small batches only");
     if (N == 0) {
         route_scan_kernel<<<1, 1024, 0, st>>>(blockhist, 0, E, 0, blocksum, cap_mode,
                                                 cap_override, r->min_capacity,
@@ -889,7 +896,7 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
     route_topk_kernel<NVV><<<nb, 1024, 0, st>>>(logits, ld, r->bias, use_pred, pred_ld,      \
                                                 pred_terms, r->b1, r->w2, r->b2, N, E, k,    \
                                                 out->indices, topp, wdst, allowed, blockhist, \
-                                                blocksum)
+                                                blocksum, ksplit, split_stride)
     if (E <= 16) YV_TOPK(1);
     else if (E <= 64) YV_TOPK(4);
     else if (E <= 128) YV_TOPK(8);
