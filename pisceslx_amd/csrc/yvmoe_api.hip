@@ -294,10 +294,12 @@ int32_t yvmoe_forward(const void* x, int32_t act_dtype, int32_t n_tokens,
     float* partials = (float*)((char*)y + y_bytes(N, k, experts->num_shared, experts->hidden, act_dtype));
     // The routing's top-k kernels sum the router's split-K partial sums themselves (in split
     // order, as the reduction of yvmoe_router_logits does), so the sums need no launch of their
-    // own; for small batches the fused routing kernel also builds the expert GEMM tile table.
+    // own (above kSmallRouteTok tokens up to kFoldSplits splits: more, read per logit, measured
+    // slower than the reduction launch); for small batches the fused routing kernel also builds
+    // the expert GEMM tile table.
     const bool small = N > 0 && N <= kSmallRouteTok;
     const int ks = router_ksplit(N, E, act_dtype, router->hidden);
-    const bool split = N > 0 && ks > 1;
+    const bool split = N > 0 && ks > 1 && (small || ks <= kFoldSplits);
     if (N > 0) {
         rc = router_gemm_launch(x, act_dtype, N, router, logits, ld, partials, st, !split);
         if (rc) return rc;

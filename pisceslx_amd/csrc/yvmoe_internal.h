@@ -50,6 +50,9 @@ inline int router_ld(int E, int act) {
 // (per-token top-k with the router's split-K reduction folded in, then everything else in
 // one work-group).
 constexpr int kSmallRouteTok = 256;
+// Most router split partial sums the multi-block top-k kernel adds itself (above
+// kSmallRouteTok tokens); more splits are reduced by a launch of their own first.
+constexpr int kFoldSplits = 4;
 
 #ifndef YV_ROUTER_KS_MAX
 // most router K splits: 16 measured best for 1-256 tokens at H = 4096, E = 64 (cfg2 decode

@@ -72,10 +72,16 @@ __global__ __launch_bounds__(1024) void route_topk_kernel(
     if (t < N) {  // uniform across the 16 lanes of a token
         int my_id;
         float my_ts, my_w0;
-        // the router GEMM's nsplit partial sums (split z at + z * sstride), summed in split order
+        // the router GEMM's nsplit (<= kFoldSplits) partial sums (split z at + z * sstride),
+        // loaded together and summed in split order
         auto split_sum = [&](const float* q) {
-            float v = q[0];
-            for (int z = 1; z < nsplit; ++z) v = v + q[z * sstride];
+            float t[kFoldSplits];
+#pragma unroll
+            for (int z = 0; z < kFoldSplits; ++z) t[z] = z < nsplit ? q[z * sstride] : 0.0f;
+            float v = t[0];
+#pragma unroll
+            for (int z = 1; z < kFoldSplits; ++z)
+                if (z < nsplit) v = v + t[z];
             return v;
         };
         topk_token<NV>([&](int e) { return split_sum(logits + (size_t)t * ld + e); }, bias, l, E, k, my_id,
@@ -882,6 +888,8 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
         YV_LAUNCH_CHECK("route_gate_loss");
     }
     YV_REQUIRE(tiles == nullptr, YVMOE_ERR_ARG, "internal: tile building is for small batches only");
+    YV_REQUIRE(ksplit >= 1 && ksplit <= kFoldSplits, YVMOE_ERR_ARG,
+               "internal: the top-k kernel sums at most %d split partial sums (got %d)", kFoldSplits, ksplit);
     if (N == 0) {
         route_scan_kernel<<<1, 1024, 0, st>>>(blockhist, 0, E, 0, blocksum, cap_mode,
                                                 cap_override, r->min_capacity,
