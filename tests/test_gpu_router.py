@@ -37,6 +37,7 @@ def _router(E, H, dev, seed):
     (1000, 2048, 128),  # ld 320: a whole and a partial column block
     (2000, 7168, 256),  # ld 448
     (4344, 5120, 128),  # cfg4's shape: 7 splits of 12 k-steps, the last of 8
+    (600, 2048, 80),    # ld 272: the last column block holds one 16-column block
     (513, 64, 16),      # K = 64: one k-step, no split
 ])
 def test_router_logits_against_float64(cuda, N, H, E):
