@@ -912,19 +912,10 @@ __global__ __launch_bounds__(64 * kWaveTok) void moegate_wave_kernel(GateArgs a)
         // ------------------------------------------------------------ SoftMoE, logits, loss
         float soft = 0.f, soft_tot = 0.f;
         if (a.mask & YVMOE_HEAD_SOFT) {
-            // torch.median: the lower middle value, the smallest value with more than (E - 1) / 2
-            // of the E values at or below it; bisection over order-preserving integer keys of
-            // the floats, counted by wavefront ballots
-            const unsigned lkb = __float_as_uint(lk);
-            const unsigned key = lkb ^ ((lkb >> 31) ? 0xffffffffu : 0x80000000u);
-            const unsigned need = (unsigned)((E - 1) / 2) + 1u;
-            unsigned lo = 0u, hi = 0xffffffffu;
-            while (lo < hi) {
-                const unsigned mid = lo + (hi - lo) / 2u;
-                if ((unsigned)__popcll(__ballot(is_e && key <= mid)) >= need) hi = mid;
-                else lo = mid + 1u;
-            }
-            const float med = __uint_as_float(lo ^ ((lo >> 31) ? 0x80000000u : 0xffffffffu));
+            // torch.median: the lower middle value, the ((E - 1) / 2)-th smallest (equal values
+            // have equal bits except +0 and -0, and either as med gives the same sigmoid below)
+            const float med = f32_from_order_key(
+                wave_kth_smallest(f32_order_key(lk), is_e, (unsigned)((E - 1) / 2)));
             const float mx = wave_max(is_e ? lv : -INFINITY);
             const float ex = is_e ? expf(lv - mx) : 0.f;
             const float se = wave_sum(ex);
