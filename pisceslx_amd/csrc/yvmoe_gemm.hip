@@ -785,9 +785,12 @@ __global__ __launch_bounds__(64 * WV) void gemm_stream_kernel(GemmParams p, int 
 // codes or bf16). Wavefronts form a 2 x 8 grid: each owns 128 activation rows and 32 weight
 // rows, reads its weight fragment once per chunk, dequantizes it to bf16(q * s) in registers
 // and multiplies it against its 8 activation row blocks (16 wavefronts, about 120 VGPRs:
-// 4 per SIMD, measured 3 % faster than 8 wavefronts of 256 x 32). For gate/up the weight
-// tile is 128 gate rows then the 128 up rows of the same columns; wavefront w holds gate and
-// up of columns 16 w .. 16 w + 15 and finishes SwiGLU in registers.
+// 4 per SIMD). int8 weights without folded rows take a 1 x 8 grid of 8 wavefronts of 256 x
+// 32 instead (about 200 VGPRs, 2 per SIMD): each weight is converted once per work-group, not
+// twice, and each wavefront converts the next chunk's weights beside its MFMAs (below) —
+// cfg3's FFN 1.3 % faster with the same bits; fp8 measured 1.7 % slower on it. For gate/up the
+// weight tile is 128 gate rows then the 128 up rows of the same columns; wavefront w holds
+// gate and up of columns 16 w .. 16 w + 15 and finishes SwiGLU in registers.
 //
 // Each lane's MFMA operands cover 16 consecutive k of the chunk (k group l / 16), split over
 // the two MFMAs of a chunk in the same order for both operands. Activation rows (128 B) are
@@ -827,7 +830,7 @@ constexpr int vmcnt_only(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 
 // FOLD: room for the kTileFold rows of a folded remainder. S4K: int4 only, the largest K whose
 // group scales the LDS table holds (8192; with folded rows 5120 beside a 3-stage ring, 8192
 // beside a 2-stage ring).
-template <int WF, int S4K = 8192, bool FOLD = false>
+template <int WF, int S4K = 8192, bool FOLD = false, int NW = 16>
 struct TileCfg {
     static constexpr bool I4 = WF == YVMOE_W_INT4;
     static constexpr int EB = (WF == YVMOE_W_BF16) ? 2 : 1;  // bytes per weight (int4: half)
@@ -839,11 +842,15 @@ struct TileCfg {
     static constexpr int B_BLK = I4 ? 512 : 1024 * EB;  // bytes of a 16-row weight block
     // 1 KB direct loads per wavefront for the 256 rows; the 32 folded rows take one 256-byte
     // dword load per wavefront, issued only by tiles that hold such rows
-    static constexpr int A_DMA = TBM * TBK * 2 / 1024 / (TTHREADS / 64);
+    static constexpr int A_DMA = TBM * TBK * 2 / 1024 / NW;
     // weight direct loads per wavefront: 1 KB each (int4: 256 B dword loads, two per block)
-    static constexpr int B_DMA = I4 ? 2 : B_BYTES / 1024 / (TTHREADS / 64);
+    static constexpr int B_DMA = I4 ? 2 : B_BYTES / 1024 / NW;
     static constexpr int NPW = A_DMA + B_DMA;
     static constexpr int S4 = I4 ? TBN * (S4K / 128) : 1;  // int4: the tile's group scales
+    // row blocks of 16 per wavefront: 16 wavefronts in a 2 x 8 grid own 128 rows each, 8 in a
+    // 1 x 8 grid all 256 (1-byte codes without folding only)
+    static constexpr int MBW = NW == 16 ? 8 : 16;
+    static_assert(NW == 16 || (NW == 8 && !FOLD && !I4 && EB == 1), "8 wavefronts: 1-byte codes, no folding");
 };
 static_assert(kTileFold * TBK * 2 == 256 * (TTHREADS / 64), "one dword load per wavefront");
 
@@ -855,9 +862,10 @@ static_assert(kTileFold * TBK * 2 == 256 * (TTHREADS / 64), "one dword load per 
 // rows. Such a launch holds two copies of the tile loop and each work-group runs the one its
 // tile needs: the copy without folded rows keeps the register use and schedule of a plain
 // tile. Launches without folding (FOLD = false) carry only that copy.
-template <int WF, int EPI, int S4K = 8192, bool FOLD = false>
-__global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int ncb) {
-    typedef TileCfg<WF, S4K, FOLD> C;
+template <int WF, int EPI, int S4K = 8192, bool FOLD = false, int NW = 16>
+__global__ __launch_bounds__(64 * NW) void gemm_tile_kernel(GemmParams p, int ncb) {
+    typedef TileCfg<WF, S4K, FOLD, NW> C;
+    constexpr int MBW = C::MBW;
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
     constexpr bool WFIRST = WF != YVMOE_W_BF16;  // weights as the MFMA's first operand
     constexpr bool GROUPED = WF == YVMOE_W_FP8;
@@ -869,7 +877,7 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
-    const int wr = wave >> 3, wc = wave & 7;  // 2 x 8 wavefronts: 128 rows x 32 weight rows each
+    const int wr = NW == 16 ? wave >> 3 : 0, wc = wave & 7;  // wavefront grid: rows x 32 weight rows
     // grouped: tiles from the tile table; dense (no table): 256-row tiles of nrows rows
     const bool dense = p.tile_seg == nullptr;
     const int ntl = dense ? (p.nrows + TBM - 1) / TBM : *p.ntiles;
@@ -930,7 +938,9 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
         int b_dst[C::B_DMA];
 #pragma unroll
         for (int j = 0; j < C::B_DMA; ++j) {
-            const int blk = wave * C::B_DMA + j;
+            // 8 wavefronts: each loads the two weight blocks it converts itself (gate/up: its gate
+            // and its up block), so its own load count says when they are in LDS
+            const int blk = (NW == 8 && SWIGLU) ? j * 8 + wave : wave * C::B_DMA + j;
             const int rb = C::I4 ? wave : blk / C::EB;           // 16-row block of the tile
             const int half = C::I4 ? j : blk % C::EB;
             const int r16 = rb * 16;
@@ -981,7 +991,7 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
         if constexpr (C::I4) {
             // the tile's group scales into LDS before any direct load is in flight
             const int kg = p.K / 128;
-            for (int i = t; i < TBN * kg; i += TTHREADS) {
+            for (int i = t; i < TBN * kg; i += 64 * NW) {
                 const int r = i / kg, q = i % kg;
                 const void* S = (SWIGLU && r >= TBN / 2) ? p.S1 : p.S0;
                 const int n = SWIGLU ? n0 + (r & (TBN / 2 - 1)) : n0 + r;
@@ -1002,13 +1012,13 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
             __syncthreads();
         }
 
-        f32x4 acc[8][2];
+        f32x4 acc[MBW][2];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < MBW; ++i) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 
         // LDS byte offsets of this lane's fragment reads (k group g = lane / 16)
         const int g = lane >> 4;
-        const int a_rd0 = swz_a(wr * 128 + (lane & 15), 2 * g), a_rd1 = swz_a(wr * 128 + (lane & 15), 2 * g + 1);
+        const int a_rd0 = swz_a(wr * MBW * 16 + (lane & 15), 2 * g), a_rd1 = swz_a(wr * MBW * 16 + (lane & 15), 2 * g + 1);
         int b_rd0[2], b_rd1[2];
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {  // piece (g, row % 16) of the row's block (+ 1 KB)
@@ -1032,7 +1042,7 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
 
         // 16-row blocks of this wavefront's 128 rows that hold rows of the segment: an expert's
         // last tile skips the MFMAs of the blocks past its end (loads and barriers stay uniform)
-        const int live_mb = min(8, max(0, (seg_end - (row0 + wr * 128) + 15) / 16));
+        const int live_mb = min(MBW, max(0, (seg_end - (row0 + wr * MBW * 16) + 15) / 16));
         // fp32 output: a wavefront whose 32 columns lie past ncols skips every MFMA (a separate
         // flag: folding it into live_mb made the compiler spill 59 VGPRs of this kernel)
         const bool colive = EPI != EPI_F32 || n0 + wc * 32 < p.ncols;
@@ -1045,6 +1055,81 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
         YV_TILE_ISSUE(0, 0);
         if (C::NST == 3 && nks > 1) YV_TILE_ISSUE(1, 1);
         int st = 0;
+        // 8 wavefronts of 256 x 32: a wavefront converts chunk c + 1's weights in the middle of
+        // chunk c, beside the MFMAs of its last 8 row blocks, as soon as its own loads of them
+        // have landed (it loads exactly the blocks it converts), so no conversion stands between
+        // a barrier and the next MFMA. One barrier per chunk, as in the 16-wavefront loop; the
+        // same MFMAs in the same order per accumulator, so the same bits.
+        if constexpr (NW == 8) {
+            auto bconv = [&](const unsigned char* Bs, int cc, bf16x8 (&bq)[2][2]) {
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+                    const u32x4 raw = *(const u32x4*)(Bs + b_rd0[nb]);
+                    const float sc = GROUPED ? lds_s[sblk[nb]][(cc * TBK) / 128] : cs[nb];
+                    Frag16 f;
+                    BLoad<WF>::cvt(make_uint4(raw.x, raw.y, raw.z, raw.w), sc, f);
+                    bq[nb][0] = f.v[0];
+                    bq[nb][1] = f.v[1];
+                }
+            };
+            const int nlm = colive ? live_mb : 0;
+            bf16x8 bcur[2][2], bnext[2][2];
+            if (nks > 1) __builtin_amdgcn_s_waitcnt(vmcnt_only(C::NPW));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+            bconv(lds_b[0], 0, bcur);
+            auto mb_step = [&](const unsigned char* As, int mb) {
+                const bf16x8 a0 = *(const bf16x8*)(As + a_rd0 + mb * 16 * 128);
+                const bf16x8 a1 = *(const bf16x8*)(As + a_rd1 + mb * 16 * 128);
+#pragma unroll
+                for (int nb = 0; nb < 2; ++nb) {
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bcur[nb][0], a0, acc[mb][nb], 0, 0, 0);
+                    acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bcur[nb][1], a1, acc[mb][nb], 0, 0, 0);
+                }
+            };
+            // NMB row blocks (8 or 16): an expert's last tile computes past its end (rows not
+            // stored) - one branch per tile instead of one per row block, whose 16 conditional
+            // blocks spilled registers
+            auto chunk = [&](auto nmb) {
+                constexpr int NMB = decltype(nmb)::value;
+                for (int c = 0; c < nks; ++c) {
+                    // every wavefront's loads of chunk c have landed (each waited for its own) and
+                    // all reads of chunk c - 1 are done: its stage takes chunk c + 2
+                    asm volatile("" ::: "memory");
+                    __builtin_amdgcn_s_barrier();
+                    asm volatile("" ::: "memory");
+                    if (c + 2 < nks) {
+                        int sn = st + 2;
+                        if (sn >= 3) sn -= 3;
+                        YV_TILE_ISSUE(c + 2, sn);
+                    }
+                    const unsigned char* As = lds_a[st];
+#pragma unroll
+                    for (int mb = 0; mb < NMB / 2; ++mb) mb_step(As, mb);
+                    int sx = st + 1;
+                    if (sx >= 3) sx -= 3;
+                    const bool more = c + 1 < nks;
+                    if (more) {
+                        // this wavefront's loads of chunk c + 1 (its weight blocks among them)
+                        if (c + 2 < nks) __builtin_amdgcn_s_waitcnt(vmcnt_only(C::NPW));
+                        else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+                        asm volatile("" ::: "memory");
+                    }
+                    // chunk c + 1's weights (after the last chunk: its own stage again, unused)
+                    bconv(lds_b[more ? sx : st], more ? c + 1 : c, bnext);
+#pragma unroll
+                    for (int mb = NMB / 2; mb < NMB; ++mb) mb_step(As, mb);
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb) {
+                        bcur[nb][0] = bnext[nb][0];
+                        bcur[nb][1] = bnext[nb][1];
+                    }
+                    st = sx;
+                }
+            };
+            if (nlm > 8) chunk(std::integral_constant<int, 16>{});
+            else if (nlm > 0) chunk(std::integral_constant<int, 8>{});
+            else chunk(std::integral_constant<int, 0>{});
+        } else
         for (int c = 0; c < nks; ++c) {
             // this wavefront's loads of chunk c have landed (the next chunk's may be in flight) ...
             if (C::NST == 3 && c + 1 < nks) {
@@ -1093,7 +1178,7 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
                     }
                 }
 #pragma unroll
-                for (int mb = 0; mb < 8; ++mb) {
+                for (int mb = 0; mb < MBW; ++mb) {
                     if (PART && mb >= live_mb) continue;
                     const bf16x8 a0 = *(const bf16x8*)(As + a_rd0 + mb * 16 * 128);
                     const bf16x8 a1 = *(const bf16x8*)(As + a_rd1 + mb * 16 * 128);
@@ -1124,7 +1209,7 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
                 }
             };
             if (xlive) compute(std::false_type{}, std::true_type{});
-            else if (live_mb == 8 && colive) compute(std::false_type{}, std::false_type{});
+            else if (live_mb == MBW && colive) compute(std::false_type{}, std::false_type{});
             else if (live_mb > 0 && colive) compute(std::true_type{}, std::false_type{});
             if (++st == C::NST) st = 0;
         }
@@ -1184,7 +1269,7 @@ __global__ __launch_bounds__(TTHREADS) void gemm_tile_kernel(GemmParams p, int n
             }
         };
 #pragma unroll
-        for (int mb = 0; mb < 8; ++mb) store_block(row0 + wr * 128 + mb * 16, acc[mb][0], acc[mb][1]);
+        for (int mb = 0; mb < MBW; ++mb) store_block(row0 + wr * MBW * 16 + mb * 16, acc[mb][0], acc[mb][1]);
         if (xlive) store_block(row0 + TBM + wr * 16, accx[0], accx[1]);
     };
     if (FOLD && ext > 0 && ext <= kTileFold) run_tile(std::integral_constant<bool, FOLD>{});
@@ -1784,7 +1869,14 @@ int tile_launch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, con
     } else {
         switch (wf) {
             case YVMOE_W_BF16: gemm_tile_kernel<YVMOE_W_BF16, EPI, 8192, FOLD><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
-            case YVMOE_W_INT8: gemm_tile_kernel<YVMOE_W_INT8, EPI, 8192, FOLD><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
+            case YVMOE_W_INT8:
+                // int8 without folding: 8 wavefronts of 256 x 32 (cfg3 FFN 4.61-4.62 -> 4.55-4.56 ms,
+                // same bits); fp8 measured 1.7 % slower on that form (cfg5)
+                if constexpr (!FOLD)
+                    gemm_tile_kernel<YVMOE_W_INT8, EPI, 8192, false, 8><<<(unsigned)blocks, 512, 0, st>>>(p, ncb);
+                else
+                    gemm_tile_kernel<YVMOE_W_INT8, EPI, 8192, FOLD><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb);
+                break;
             case YVMOE_W_FP8: gemm_tile_kernel<YVMOE_W_FP8, EPI, 8192, FOLD><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
             case YVMOE_W_INT4:
                 if (p.K > 8192) {  // the group-scale table in LDS holds K / 128 <= 64 groups
