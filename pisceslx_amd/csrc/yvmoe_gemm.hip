@@ -109,6 +109,7 @@ struct GemmParams {
     long long split_stride;  // output elements between splits (EPI_F32 partial sums)
     const float* col_bias;   // EPI_F32: added to columns < col_bias_n by split 0 (or NULL)
     int col_bias_n;
+    int nshared;             // shared experts (their tiles end the table; streaming WS form)
 };
 
 // EPI_F32 output value of column n for split kz: the accumulator plus the column bias.
@@ -760,18 +761,48 @@ __device__ __forceinline__ void stream_item(const GemmParams& p, int tile, int c
 // contiguous ranges, one per XCD: the tiles that share weights (the 16-row tiles of a shared
 // expert, which all read the same columns) then run together on one XCD and fetch those
 // weights from HBM once into its L2 instead of once per tile.
-template <int WF, int EPI, int U, int MAXRB, int NB, bool PF = false, int WV = 4>
+//
+// WS (16-row tiles only): the rows of shared experts (from routed_rows on, every token) run 64
+// at a time on the 64-row form (one k-step per staged chunk, the next chunk's weights in
+// flight: the same LDS as the 16-row form), so each shared weight is read and converted once
+// per column group instead of once per 16-row tile. Those items take the first work-group ids
+// and so start first: they are slower per item than the 16-row items (a barrier per k-step),
+// and last in the launch they set its end (cfg2 decode layer step 214.4 -> 253.4 us when they
+// kept their places among the tiles, 214.4 -> 207.5 us first; the same bits either way).
+template <int WF, int EPI, int U, int MAXRB, int NB, bool PF = false, int WV = 4, bool WS = false>
 __global__ __launch_bounds__(64 * WV) void gemm_stream_kernel(GemmParams p, int ngroups, int nsplit) {
-    __shared__ uint4 As[2][16 * MAXRB * (U * 8 + 1)];
-    const int nt = p.tile_seg == nullptr ? (p.nrows + 16 * MAXRB - 1) / (16 * MAXRB) : *p.ntiles;
+    constexpr int A_N = 2 * 16 * MAXRB * (U * 8 + 1);
+    constexpr int A_W = WS ? 2 * 64 * 9 : 0;
+    __shared__ uint4 As_raw[A_N > A_W ? A_N : A_W];
+    static_assert(!WS || MAXRB == 1, "wide shared rows beside 16-row tiles only");
+    int nt = p.tile_seg == nullptr ? (p.nrows + 16 * MAXRB - 1) / (16 * MAXRB) : *p.ntiles;
+    int b = blockIdx.x;
+    if constexpr (WS) {
+        // the first work-groups take the 64-row items of the shared experts (so they start
+        // first), the rest the 16-row items of the routed tiles
+        const int tps = (p.ntok + 15) / 16, lps = (p.ntok + 63) / 64;  // tiles, 64-row items per expert
+        const int nlead = p.nshared * lps;
+        const int nwide = nlead * ngroups * nsplit;
+        nt -= p.nshared * tps;  // routed tiles
+        if (b < nwide) {
+            const int lead = b % nlead, rest = b / nlead;
+            const int tile = nt + (lead / lps) * tps + (lead % lps) * 4;
+            stream_item<WF, EPI, 1, 4, NB, true, WV>(p, tile, rest % ngroups, rest / ngroups,
+                                                     *reinterpret_cast<uint4(*)[2][64 * 9]>(As_raw));
+            return;
+        }
+        b -= nwide;
+    }
     const int nitems = nt * ngroups * nsplit;
     const int per_xcd = (nitems + 7) / 8;
-    const int local = blockIdx.x / 8;
+    const int local = b / 8;
     if (local >= per_xcd) return;
-    const int item = (blockIdx.x % 8) * per_xcd + local;
+    const int item = (b % 8) * per_xcd + local;
     if (item >= nitems) return;
     const int rest = item / nt;  // tile fastest, then column group, then K split
-    stream_item<WF, EPI, U, MAXRB, NB, PF, WV>(p, item % nt, rest % ngroups, rest / ngroups, As);
+    const int tile = item % nt;
+    stream_item<WF, EPI, U, MAXRB, NB, PF, WV>(p, tile, rest % ngroups, rest / ngroups,
+                                               *reinterpret_cast<uint4(*)[2][16 * MAXRB * (U * 8 + 1)]>(As_raw));
 }
 
 // ------------------------------------------------------------------ bf16, LDS-tiled form
@@ -1795,13 +1826,14 @@ int reduce_splits_launch(const float* part, int nsplit, long long n, float* out,
 
 // Streaming (decode) form: one (tile, column group) item per work-group; NB 16-column
 // blocks per wavefront.
-template <int EPI, int U, int NB, int MAXRB = 1, bool PF = false, int WV = 4>
+template <int EPI, int U, int NB, int MAXRB = 1, bool PF = false, int WV = 4, bool WS = false>
 int stream_dispatch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, const char* name,
                     int nsplit = 1) {
     const int ngroups = (EPI == EPI_SWIGLU) ? ceil_div(p.ncols, 8 * WV * NB) : ceil_div(p.ncols, 16 * WV * NB);
-    const long long items = 8LL * ceil_div(ntiles_max * ngroups * nsplit, 8);
+    long long items = 8LL * ceil_div(ntiles_max * ngroups * nsplit, 8);
+    if constexpr (WS) items += (long long)p.nshared * ceil_div(p.ntok, 64) * ngroups * nsplit;
     if (items <= 0) return YVMOE_OK;
-#define YV_ST(WFV) gemm_stream_kernel<WFV, EPI, U, MAXRB, NB, PF, WV><<<(unsigned)items, 64 * WV, 0, st>>>(p, ngroups, nsplit)
+#define YV_ST(WFV) gemm_stream_kernel<WFV, EPI, U, MAXRB, NB, PF, WV, WS><<<(unsigned)items, 64 * WV, 0, st>>>(p, ngroups, nsplit)
     if constexpr (EPI == EPI_F32) {  // dense fp32 output: bf16 weights only
         if (wf != YVMOE_W_BF16) {
             set_error("%s: fp32-output streaming form needs bf16 weights", name);
@@ -2135,6 +2167,7 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.rowdiv = k;
     p.routed_rows = N * k;
     p.ntok = N;
+    p.nshared = S;
     p.B0 = w->w_gate;
     p.B1 = w->w_up;
     p.S0 = w->s_gate;
@@ -2150,7 +2183,9 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
     p.kchunk = H;
     const bool streaming = (maxrb == 1);
     int rc = tiled ? tile_dispatch<EPI_SWIGLU>(wf, p, T, st, "expert_gemm1", tt.fold > 0)
-           : streaming ? stream_dispatch<EPI_SWIGLU, YV_U1, YV_NB1, 1, YV_PF1, YV_WV1>(wf, p, T, st, "expert_gemm1")
+           : streaming ? (S > 0
+                              ? stream_dispatch<EPI_SWIGLU, YV_U1, YV_NB1, 1, YV_PF1, YV_WV1, true>(wf, p, T, st, "expert_gemm1")
+                              : stream_dispatch<EPI_SWIGLU, YV_U1, YV_NB1, 1, YV_PF1, YV_WV1>(wf, p, T, st, "expert_gemm1"))
                        : gemm_dispatch<EPI_SWIGLU>(act, wf, p, T, (F % 32 == 0) ? 2 : 1, 1, st,
                                                    "expert_gemm1", maxrb);
     if (rc != YVMOE_OK) return rc;
@@ -2180,7 +2215,9 @@ int expert_ffn_launch(const void* x, int act, int N, int k, const yvmoe_expert_w
         if (rc != YVMOE_OK || tt.light == 0) return rc;
         return light_launch(p, std::integral_constant<int, EPI_DOWN>{}, "expert_gemm2_light");
     }
-    return streaming ? stream_dispatch<EPI_DOWN, YV_U2, YV_NB2, 1, YV_PF2, YV_WV2>(wf, p, T, st, "expert_gemm2")
+    return streaming ? (S > 0
+                            ? stream_dispatch<EPI_DOWN, YV_U2, YV_NB2, 1, YV_PF2, YV_WV2, true>(wf, p, T, st, "expert_gemm2")
+                            : stream_dispatch<EPI_DOWN, YV_U2, YV_NB2, 1, YV_PF2, YV_WV2>(wf, p, T, st, "expert_gemm2"))
                      : gemm_dispatch<EPI_DOWN>(act, wf, p, T, (H % 32 == 0) ? 2 : 1, 1, st,
                                                "expert_gemm2", maxrb);
 }
