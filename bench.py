@@ -33,7 +33,7 @@ routing): layer step and grouped FFN, the FFN against both rooflines; cfg5 also 
 realised expert load against the Zipf(1.2) target (KL).
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
-       python bench.py --pmc-probe {cfg2,cfg3,cfg5,moegate}   (launches only, for counter runs)
+       python bench.py --pmc-probe {cfg2,cfg3,cfg5,moegate,moegate_decode}   (launches only, for counter runs)
 """
 import argparse
 import dataclasses
@@ -67,7 +67,7 @@ def parse():
     ap.add_argument("--no-norm", action="store_true", help="skip the MoE input RMSNorm timing")
     ap.add_argument("--no-other-configs", action="store_true",
                     help="skip cfg1 / cfg4 / cfg5 (layer step and FFN against both rooflines)")
-    ap.add_argument("--pmc-probe", choices=["cfg2", "cfg3", "cfg5", "moegate"], default=None,
+    ap.add_argument("--pmc-probe", choices=["cfg2", "cfg3", "cfg5", "moegate", "moegate_decode"], default=None,
                     help="run the calibration copy and 5 expert-FFN launches (moegate: 3 YvMoEGate "
                          "prefill gate calls), nothing timed")
     return ap.parse_args()
@@ -86,22 +86,27 @@ def pmc_probe(name):
         torch.bitwise_not(src, out=dst)
     torch.cuda.synchronize()
     del src, dst
-    if name == "moegate":  # the prefill gate call of bench's "moegate" object
+    if name in ("moegate", "moegate_decode"):  # the prefill / decode gate call of "moegate"
         import dataclasses
         from pisceslx_amd import _lib
         from pisceslx_amd.gate import YvMoEGate
-        from pisceslx_amd.workloads import seq_lengths
-        spec = make_workload("cfg2", device="cuda", seed=0).spec
-        N = sum(seq_lengths("cfg3", 0))
+        from pisceslx_amd.workloads import SPECS, seq_lengths
+        spec = SPECS["cfg2"]
+        decode = name == "moegate_decode"
+        N = 64 if decode else sum(seq_lengths("cfg3", 0))
         torch.manual_seed(0)
         g = YvMoEGate(spec.hidden, spec.num_experts, top_k=spec.top_k, device="cuda",
                       dtype=torch.bfloat16).eval()
         x = torch.randn(N, spec.hidden, device="cuda",
                         generator=torch.Generator(device="cuda").manual_seed(3)).to(torch.bfloat16)
-        st0 = g.gate_state(_lib.ACT_BF16, N)
+        st0 = g.gate_state(_lib.ACT_BF16, 1 if decode else N)
+        # decode: three copies of the projection operand in turn, as the timed bench does, so
+        # the 256 MB Infinity Cache does not serve one call's weights from the call before
+        states = [st0] + ([dataclasses.replace(st0, w_proj=st0.w_proj.clone()) for _ in range(2)]
+                          if decode else [])
         ws = torch.empty(1 << 31, dtype=torch.uint8, device="cuda")
-        for _ in range(3):
-            yvf.moegate_forward(x, st0, spec.top_k, workspace=ws)
+        for i in range(6 if decode else 3):
+            yvf.moegate_forward(x, states[i % len(states)], spec.top_k, workspace=ws)
         torch.cuda.synchronize()
         print(f"pmc probe {name}: done", flush=True)
         return
