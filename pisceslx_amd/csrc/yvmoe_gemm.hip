@@ -57,6 +57,12 @@
 #ifndef YV_U2
 #define YV_U2 4  // k-steps per staged chunk, streaming down projection
 #endif
+#ifndef YV_PTILE
+// persistent 8-wavefront int8 tile form (the next item's first chunks loaded during the current
+// item's last chunk and epilogue): 0 off, 1 down projection only, 2 both projections. cfg3 FFN on
+// alternating runs, same bits: 2 -1.0 / -1.3 / -1.4 %; 1 and gate/up alone ±0
+#define YV_PTILE 2
+#endif
 
 namespace yvmoe {
 namespace {
@@ -1307,6 +1313,206 @@ __global__ __launch_bounds__(64 * NW) void gemm_tile_kernel(GemmParams p, int nc
     else run_tile(std::false_type{});
 }
 
+// Persistent form of the 8-wavefront int8 tile kernel (no folded rows, K of at least 3 chunks):
+// one work-group per CU walks its XCD's range of (tile, column block) items with the stride of
+// that XCD's work-groups, so the work-groups of an XCD still run neighbouring items together.
+// After the barrier that opens an item's last chunk, the two ring stages that chunk does not
+// use are free: they take the next item's chunks 0 and 1, which land during the last chunk's
+// MFMAs and the epilogue instead of after a new work-group's start. The arithmetic per item is
+// the 8-wavefront loop of gemm_tile_kernel (the same bits).
+template <int EPI>
+__global__ __launch_bounds__(512) void gemm_tile_persist_kernel(GemmParams p, int ncb) {
+    typedef TileCfg<YVMOE_W_INT8, 8192, false, 8> C;
+    constexpr int MBW = C::MBW;
+    constexpr bool SWIGLU = EPI == EPI_SWIGLU;
+    constexpr long long B_CHUNK = C::B_BLK;
+    __shared__ __attribute__((aligned(1024))) unsigned char lds_a[3][C::A_BYTES];
+    __shared__ __attribute__((aligned(1024))) unsigned char lds_b[3][C::B_BYTES];
+    const int t = threadIdx.x;
+    const int lane = t & 63;
+    const int wave = t >> 6;
+    const int wc = wave;
+    const int total = *p.ntiles * ncb;
+    const int per_xcd = (total + 7) / 8;
+    const int xend = min(total, (int)(blockIdx.x % 8) * per_xcd + per_xcd);
+    const int stride = gridDim.x / 8;
+    int item = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+    if (item >= xend) return;
+    const int nks = p.K / TBK;
+
+    // item-independent: weight block of each direct load, fragment rows and LDS read offsets
+    int b_blk[C::B_DMA];
+#pragma unroll
+    for (int j = 0; j < C::B_DMA; ++j) b_blk[j] = SWIGLU ? j * 8 + wave : wave * C::B_DMA + j;
+    int brow[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+        const int i = lane & 15, q = i >> 2;
+        brow[nb] = SWIGLU ? nb * (TBN / 2) + wc * 16 + i : wc * 32 + q * 8 + 4 * ((q >> 1) ^ nb) + (i & 3);
+    }
+    const int g = lane >> 4;
+    const int a_rd0 = swz_a(lane & 15, 2 * g), a_rd1 = swz_a(lane & 15, 2 * g + 1);
+    int b_rd0[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) b_rd0[nb] = (brow[nb] >> 4) * C::B_BLK + (16 * g + (brow[nb] & 15)) * 16;
+
+    // one item's addressing: direct-load sources and the two per-column scales
+    struct Item {
+        int row0, seg_end, n0;
+        const char* a_src[C::A_DMA];
+        const char* b_src[C::B_DMA];
+        float cs[2];
+    };
+    auto setup = [&](int it, Item& I) {
+        const int tile = it / ncb, cb = it % ncb;
+        const int e = p.tile_seg[tile];
+        I.row0 = p.tile_row0[tile];
+        I.seg_end = p.seg_start[e + 1];
+        I.n0 = SWIGLU ? cb * (TBN / 2) : cb * TBN;
+        const long long e_off = (long long)e * p.b_stride;
+        const long long s_off = (long long)e * p.s_stride;
+#pragma unroll
+        for (int j = 0; j < C::A_DMA; ++j) {
+            const int blk = wave * C::A_DMA + j;
+            const int r = blk * 8 + lane / 8;
+            const int lc = (lane % 8) ^ (lane / 8) ^ (blk & 1);
+            const int gr = (I.row0 + r < I.seg_end) ? I.row0 + r : I.row0;
+            I.a_src[j] = (const char*)p.A + ((long long)map_row(p, gr) * p.lda + lc * 8) * 2;
+        }
+#pragma unroll
+        for (int j = 0; j < C::B_DMA; ++j) {
+            const int r16 = b_blk[j] * 16;
+            const void* B = (SWIGLU && r16 >= TBN / 2) ? p.B1 : p.B0;
+            const int nb16 = SWIGLU ? I.n0 + (r16 & (TBN / 2 - 1)) : I.n0 + r16;
+            I.b_src[j] = (const char*)B + e_off + (long long)(nb16 >> 4) * (p.K / 64) * B_CHUNK + lane * 16;
+        }
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+            const int r = brow[nb];
+            const void* S = (SWIGLU && r >= TBN / 2) ? p.S1 : p.S0;
+            I.cs[nb] = b_scale<YVMOE_W_INT8>(S, s_off, SWIGLU ? I.n0 + (r & (TBN / 2 - 1)) : I.n0 + r, p.K, 0);
+        }
+    };
+    auto issue = [&](const Item& I, int chunk, int st) {
+#pragma unroll
+        for (int j = 0; j < C::A_DMA; ++j)
+            dma16(I.a_src[j] + (size_t)chunk * TBK * 2, &lds_a[st][(wave * C::A_DMA + j) * 1024]);
+#pragma unroll
+        for (int j = 0; j < C::B_DMA; ++j) dma16(I.b_src[j] + (size_t)chunk * B_CHUNK, &lds_b[st][b_blk[j] * 1024]);
+    };
+
+    Item cur, nxt;
+    setup(item, cur);
+    int st = 0;
+    issue(cur, 0, 0);
+    issue(cur, 1, 1);
+    for (;;) {
+        const int next = item + stride;
+        const bool has_next = next < xend;
+        if (has_next) setup(next, nxt);
+        f32x4 acc[MBW][2];
+#pragma unroll
+        for (int i = 0; i < MBW; ++i) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+        auto bconv = [&](const unsigned char* Bs, bf16x8 (&bq)[2][2]) {
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                const u32x4 raw = *(const u32x4*)(Bs + b_rd0[nb]);
+                Frag16 f;
+                BLoad<YVMOE_W_INT8>::cvt(make_uint4(raw.x, raw.y, raw.z, raw.w), cur.cs[nb], f);
+                bq[nb][0] = f.v[0];
+                bq[nb][1] = f.v[1];
+            }
+        };
+        const int live_mb = min(MBW, max(0, (cur.seg_end - cur.row0 + 15) / 16));
+        bf16x8 bcur[2][2], bnext[2][2];
+        // chunk 0 of this item has landed (chunk 1's loads, the younger ones, may be in flight)
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(C::NPW));
+        bconv(lds_b[st], bcur);
+        auto mb_step = [&](const unsigned char* As, int mb) {
+            const bf16x8 a0 = *(const bf16x8*)(As + a_rd0 + mb * 16 * 128);
+            const bf16x8 a1 = *(const bf16x8*)(As + a_rd1 + mb * 16 * 128);
+#pragma unroll
+            for (int nb = 0; nb < 2; ++nb) {
+                acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bcur[nb][0], a0, acc[mb][nb], 0, 0, 0);
+                acc[mb][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bcur[nb][1], a1, acc[mb][nb], 0, 0, 0);
+            }
+        };
+        auto chunk = [&](auto nmb) {
+            constexpr int NMB = decltype(nmb)::value;
+            for (int c = 0; c < nks; ++c) {
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_s_barrier();
+                asm volatile("" ::: "memory");
+                int s1 = st + 1;
+                if (s1 >= 3) s1 -= 3;
+                int s2 = st + 2;
+                if (s2 >= 3) s2 -= 3;
+                if (c + 2 < nks) {
+                    issue(cur, c + 2, s2);
+                } else if (c + 1 == nks && has_next) {
+                    // the stages of chunks c - 2 and c - 1 are free: the next item's chunks 0, 1
+                    issue(nxt, 0, s1);
+                    issue(nxt, 1, s2);
+                }
+                const unsigned char* As = lds_a[st];
+#pragma unroll
+                for (int mb = 0; mb < NMB / 2; ++mb) mb_step(As, mb);
+                const bool more = c + 1 < nks;
+                if (more) {
+                    if (c + 2 < nks) __builtin_amdgcn_s_waitcnt(vmcnt_only(C::NPW));
+                    else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+                    asm volatile("" ::: "memory");
+                    bconv(lds_b[s1], bnext);
+                }
+#pragma unroll
+                for (int mb = NMB / 2; mb < NMB; ++mb) mb_step(As, mb);
+                if (more) {
+#pragma unroll
+                    for (int nb = 0; nb < 2; ++nb) {
+                        bcur[nb][0] = bnext[nb][0];
+                        bcur[nb][1] = bnext[nb][1];
+                    }
+                }
+                st = s1;
+            }
+        };
+        if (live_mb > 8) chunk(std::integral_constant<int, 16>{});
+        else if (live_mb > 0) chunk(std::integral_constant<int, 8>{});
+        else chunk(std::integral_constant<int, 0>{});
+
+        // epilogue (gemm_tile_kernel's WFIRST store_block)
+        const int seg_end = cur.seg_end, n0 = cur.n0;
+        auto store_block = [&](int rb, f32x4 c0, f32x4 c1) {
+            const int r = rb + (lane & 15);
+            if (r >= seg_end) return;
+            if constexpr (SWIGLU) {
+                const int n = n0 + wc * 16 + 4 * g;
+                float hv[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float gt = round_bf16(c0[i]);
+                    const float up = round_bf16(c1[i]);
+                    hv[i] = round_bf16(silu(gt)) * up;
+                }
+                *(uint2*)((unsigned short*)p.out + (long long)r * p.ldo + n) =
+                    make_uint2(pack_bf16(hv[0], hv[1]), pack_bf16(hv[2], hv[3]));
+            } else {
+                const int n = n0 + wc * 32 + 8 * g;
+                const f32x4 lo = g < 2 ? c0 : c1;
+                const f32x4 hi = g < 2 ? c1 : c0;
+                *(uint4*)((unsigned short*)p.out + (long long)r * p.ldo + n) =
+                    make_uint4(pack_bf16(lo[0], lo[1]), pack_bf16(lo[2], lo[3]),
+                               pack_bf16(hi[0], hi[1]), pack_bf16(hi[2], hi[3]));
+            }
+        };
+#pragma unroll
+        for (int mb = 0; mb < MBW; ++mb) store_block(cur.row0 + mb * 16, acc[mb][0], acc[mb][1]);
+        if (!has_next) break;
+        item = next;
+        cur = nxt;
+    }
+}
+
 // ------------------------------------------------------------------ bf16, wide dense form
 // Dense fp32-output GEMM over many tiles (the YvMoEGate projection at prefill): out[N][ldo] =
 // x[N][K] · Wᵀ (+ a column bias), W [ncols][K] bf16 in the 16 x 64 block order.
@@ -1903,10 +2109,14 @@ int tile_launch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, con
             case YVMOE_W_BF16: gemm_tile_kernel<YVMOE_W_BF16, EPI, 8192, FOLD><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
             case YVMOE_W_INT8:
                 // int8 without folding: 8 wavefronts of 256 x 32 (cfg3 FFN 4.61-4.62 -> 4.55-4.56 ms,
-                // same bits); fp8 measured 1.7 % slower on that form (cfg5)
-                if constexpr (!FOLD)
-                    gemm_tile_kernel<YVMOE_W_INT8, EPI, 8192, false, 8><<<(unsigned)blocks, 512, 0, st>>>(p, ncb);
-                else
+                // same bits; fp8 measured 1.7 % slower on that form, cfg5), one persistent
+                // work-group per CU (YV_PTILE)
+                if constexpr (!FOLD) {
+                    if ((YV_PTILE == 2 || (YV_PTILE == 1 && EPI == EPI_DOWN)) && p.K / TBK >= 3)
+                        gemm_tile_persist_kernel<EPI><<<(unsigned)std::min<long long>(blocks, 256), 512, 0, st>>>(p, ncb);
+                    else
+                        gemm_tile_kernel<YVMOE_W_INT8, EPI, 8192, false, 8><<<(unsigned)blocks, 512, 0, st>>>(p, ncb);
+                } else
                     gemm_tile_kernel<YVMOE_W_INT8, EPI, 8192, FOLD><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb);
                 break;
             case YVMOE_W_FP8: gemm_tile_kernel<YVMOE_W_FP8, EPI, 8192, FOLD><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
