@@ -63,6 +63,11 @@
 // alternating runs, same bits: 2 -1.0 / -1.3 / -1.4 %; 1 and gate/up alone ±0
 #define YV_PTILE 2
 #endif
+#ifndef YV_PFP8
+// fp8 on the persistent 8-wavefront form (block scales from a per-item LDS table): cfg5 FFN
+// 6.86-6.87 -> 6.99 ms on alternating runs, same bits; off
+#define YV_PFP8 0
+#endif
 
 namespace yvmoe {
 namespace {
@@ -1320,14 +1325,18 @@ __global__ __launch_bounds__(64 * NW) void gemm_tile_kernel(GemmParams p, int nc
 // use are free: they take the next item's chunks 0 and 1, which land during the last chunk's
 // MFMAs and the epilogue instead of after a new work-group's start. The arithmetic per item is
 // the 8-wavefront loop of gemm_tile_kernel (the same bits).
-template <int EPI>
+template <int WF, int EPI>
 __global__ __launch_bounds__(512) void gemm_tile_persist_kernel(GemmParams p, int ncb) {
-    typedef TileCfg<YVMOE_W_INT8, 8192, false, 8> C;
+    typedef TileCfg<WF, 8192, false, 8> C;
+    static_assert(WF == YVMOE_W_INT8 || WF == YVMOE_W_FP8, "1-byte codes");
     constexpr int MBW = C::MBW;
     constexpr bool SWIGLU = EPI == EPI_SWIGLU;
+    constexpr bool GROUPED = WF == YVMOE_W_FP8;
     constexpr long long B_CHUNK = C::B_BLK;
     __shared__ __attribute__((aligned(1024))) unsigned char lds_a[3][C::A_BYTES];
     __shared__ __attribute__((aligned(1024))) unsigned char lds_b[3][C::B_BYTES];
+    // fp8: block scales of the item's two 128-row weight blocks, one table per item in turn
+    __shared__ float lds_s[GROUPED ? 2 : 1][2][64];
     const int t = threadIdx.x;
     const int lane = t & 63;
     const int wave = t >> 6;
@@ -1356,14 +1365,19 @@ __global__ __launch_bounds__(512) void gemm_tile_persist_kernel(GemmParams p, in
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) b_rd0[nb] = (brow[nb] >> 4) * C::B_BLK + (16 * g + (brow[nb] & 15)) * 16;
 
-    // one item's addressing: direct-load sources and the two per-column scales
+    int sblk[2];  // fp8: which of the item's two scale blocks each fragment's rows use
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) sblk[nb] = brow[nb] / 128;
+
+    // one item's addressing: direct-load sources and the two per-column scales (int8) or the
+    // index of its block-scale table (fp8)
     struct Item {
-        int row0, seg_end, n0;
+        int row0, seg_end, n0, sbuf;
         const char* a_src[C::A_DMA];
         const char* b_src[C::B_DMA];
         float cs[2];
     };
-    auto setup = [&](int it, Item& I) {
+    auto setup = [&](int it, Item& I, int sbuf) {
         const int tile = it / ncb, cb = it % ncb;
         const int e = p.tile_seg[tile];
         I.row0 = p.tile_row0[tile];
@@ -1386,11 +1400,24 @@ __global__ __launch_bounds__(512) void gemm_tile_persist_kernel(GemmParams p, in
             const int nb16 = SWIGLU ? I.n0 + (r16 & (TBN / 2 - 1)) : I.n0 + r16;
             I.b_src[j] = (const char*)B + e_off + (long long)(nb16 >> 4) * (p.K / 64) * B_CHUNK + lane * 16;
         }
+        I.sbuf = sbuf;
+        if constexpr (GROUPED) {
+            // written a whole item before its first reader (the current item's barriers
+            // publish it); the table it replaces belonged to the item before the current one
+            I.cs[0] = I.cs[1] = 1.0f;
+            const int kb = p.K / 128;
+            if (t < 2 * kb) {
+                const int b = t / kb, q = t % kb;
+                const void* S = (SWIGLU && b == 1) ? p.S1 : p.S0;
+                lds_s[sbuf][b][q] = b_scale<WF>(S, s_off, SWIGLU ? I.n0 : I.n0 + b * 128, p.K, q * 128);
+            }
+        } else {
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) {
-            const int r = brow[nb];
-            const void* S = (SWIGLU && r >= TBN / 2) ? p.S1 : p.S0;
-            I.cs[nb] = b_scale<YVMOE_W_INT8>(S, s_off, SWIGLU ? I.n0 + (r & (TBN / 2 - 1)) : I.n0 + r, p.K, 0);
+            for (int nb = 0; nb < 2; ++nb) {
+                const int r = brow[nb];
+                const void* S = (SWIGLU && r >= TBN / 2) ? p.S1 : p.S0;
+                I.cs[nb] = b_scale<WF>(S, s_off, SWIGLU ? I.n0 + (r & (TBN / 2 - 1)) : I.n0 + r, p.K, 0);
+            }
         }
     };
     auto issue = [&](const Item& I, int chunk, int st) {
@@ -1402,23 +1429,25 @@ __global__ __launch_bounds__(512) void gemm_tile_persist_kernel(GemmParams p, in
     };
 
     Item cur, nxt;
-    setup(item, cur);
+    setup(item, cur, 0);
     int st = 0;
     issue(cur, 0, 0);
     issue(cur, 1, 1);
+    if constexpr (GROUPED) __syncthreads();  // the first item's scale table
     for (;;) {
         const int next = item + stride;
         const bool has_next = next < xend;
-        if (has_next) setup(next, nxt);
+        if (has_next) setup(next, nxt, cur.sbuf ^ 1);
         f32x4 acc[MBW][2];
 #pragma unroll
         for (int i = 0; i < MBW; ++i) acc[i][0] = acc[i][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-        auto bconv = [&](const unsigned char* Bs, bf16x8 (&bq)[2][2]) {
+        auto bconv = [&](const unsigned char* Bs, int cc, bf16x8 (&bq)[2][2]) {
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) {
                 const u32x4 raw = *(const u32x4*)(Bs + b_rd0[nb]);
+                const float sc = GROUPED ? lds_s[cur.sbuf][sblk[nb]][(cc * TBK) / 128] : cur.cs[nb];
                 Frag16 f;
-                BLoad<YVMOE_W_INT8>::cvt(make_uint4(raw.x, raw.y, raw.z, raw.w), cur.cs[nb], f);
+                BLoad<WF>::cvt(make_uint4(raw.x, raw.y, raw.z, raw.w), sc, f);
                 bq[nb][0] = f.v[0];
                 bq[nb][1] = f.v[1];
             }
@@ -1427,7 +1456,7 @@ __global__ __launch_bounds__(512) void gemm_tile_persist_kernel(GemmParams p, in
         bf16x8 bcur[2][2], bnext[2][2];
         // chunk 0 of this item has landed (chunk 1's loads, the younger ones, may be in flight)
         __builtin_amdgcn_s_waitcnt(vmcnt_only(C::NPW));
-        bconv(lds_b[st], bcur);
+        bconv(lds_b[st], 0, bcur);
         auto mb_step = [&](const unsigned char* As, int mb) {
             const bf16x8 a0 = *(const bf16x8*)(As + a_rd0 + mb * 16 * 128);
             const bf16x8 a1 = *(const bf16x8*)(As + a_rd1 + mb * 16 * 128);
@@ -1462,7 +1491,7 @@ __global__ __launch_bounds__(512) void gemm_tile_persist_kernel(GemmParams p, in
                     if (c + 2 < nks) __builtin_amdgcn_s_waitcnt(vmcnt_only(C::NPW));
                     else __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
                     asm volatile("" ::: "memory");
-                    bconv(lds_b[s1], bnext);
+                    bconv(lds_b[s1], c + 1, bnext);
                 }
 #pragma unroll
                 for (int mb = NMB / 2; mb < NMB; ++mb) mb_step(As, mb);
@@ -2113,13 +2142,21 @@ int tile_launch(int wf, const GemmParams& p, int ntiles_max, hipStream_t st, con
                 // work-group per CU (YV_PTILE)
                 if constexpr (!FOLD) {
                     if ((YV_PTILE == 2 || (YV_PTILE == 1 && EPI == EPI_DOWN)) && p.K / TBK >= 3)
-                        gemm_tile_persist_kernel<EPI><<<(unsigned)std::min<long long>(blocks, 256), 512, 0, st>>>(p, ncb);
+                        gemm_tile_persist_kernel<YVMOE_W_INT8, EPI><<<(unsigned)std::min<long long>(blocks, 256), 512, 0, st>>>(p, ncb);
                     else
                         gemm_tile_kernel<YVMOE_W_INT8, EPI, 8192, false, 8><<<(unsigned)blocks, 512, 0, st>>>(p, ncb);
                 } else
                     gemm_tile_kernel<YVMOE_W_INT8, EPI, 8192, FOLD><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb);
                 break;
-            case YVMOE_W_FP8: gemm_tile_kernel<YVMOE_W_FP8, EPI, 8192, FOLD><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb); break;
+            case YVMOE_W_FP8:
+                if constexpr (!FOLD) {
+                    if (YV_PFP8 && p.K / TBK >= 3 && p.K <= 8192) {
+                        gemm_tile_persist_kernel<YVMOE_W_FP8, EPI><<<(unsigned)std::min<long long>(blocks, 256), 512, 0, st>>>(p, ncb);
+                        break;
+                    }
+                }
+                gemm_tile_kernel<YVMOE_W_FP8, EPI, 8192, FOLD><<<(unsigned)blocks, TTHREADS, 0, st>>>(p, ncb);
+                break;
             case YVMOE_W_INT4:
                 if (p.K > 8192) {  // the group-scale table in LDS holds K / 128 <= 64 groups
                     set_error("%s: tiled int4 form needs K <= 8192 (K=%d)", name, p.K);
