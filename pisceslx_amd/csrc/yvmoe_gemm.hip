@@ -1318,13 +1318,15 @@ __global__ __launch_bounds__(64 * NW) void gemm_tile_kernel(GemmParams p, int nc
     else run_tile(std::false_type{});
 }
 
-// Persistent form of the 8-wavefront int8 tile kernel (no folded rows, K of at least 3 chunks):
+// Persistent form of the 8-wavefront tile kernel for 1-byte codes (int8; fp8 measured slower on
+// it and stays on gemm_tile_kernel's 16 wavefronts), no folded rows, K of at least 3 chunks:
 // one work-group per CU walks its XCD's range of (tile, column block) items with the stride of
 // that XCD's work-groups, so the work-groups of an XCD still run neighbouring items together.
 // After the barrier that opens an item's last chunk, the two ring stages that chunk does not
 // use are free: they take the next item's chunks 0 and 1, which land during the last chunk's
 // MFMAs and the epilogue instead of after a new work-group's start. The arithmetic per item is
-// the 8-wavefront loop of gemm_tile_kernel (the same bits).
+// the 8-wavefront loop of gemm_tile_kernel (the same bits). The next item's first wait also
+// covers the epilogue's stores (they count in the same counter as the loads).
 template <int WF, int EPI>
 __global__ __launch_bounds__(512) void gemm_tile_persist_kernel(GemmParams p, int ncb) {
     typedef TileCfg<WF, 8192, false, 8> C;
