@@ -77,5 +77,59 @@ __device__ __forceinline__ void gate_loss_block(const GateLossArgs& a) {
     }
 }
 
+// Split form of gate_loss_block for at most 64 groups (the small-batch routing kernel): the
+// loads go out with the caller's first loads (gate_loss_load, lane l of wavefront w holding
+// group l of columns w, w + 16, ...), and the sums run later (gate_loss_finish, every thread,
+// barriers inside) with gate_loss_block's arithmetic: each column's sum is 0 + its lane's value
+// (gate_loss_block's further terms are zeros at this size), then the same wave reduction.
+constexpr int kLossCols = (YVMOE_MAX_EXPERTS + 2 + 15) / 16;
+struct LossRegs {
+    float v[kLossCols];
+};
+__device__ __forceinline__ void gate_loss_load(const GateLossArgs& a, LossRegs& r) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < kLossCols; ++i) {
+        const int c = wave + 16 * i;
+        r.v[i] = (c < a.E + 2 && lane < a.G) ? a.part[(long long)c * a.G + lane] : 0.f;
+    }
+}
+__device__ __forceinline__ void gate_loss_finish(const GateLossArgs& a, const LossRegs& r) {
+    __shared__ float col[YVMOE_MAX_EXPERTS + 2];
+    __shared__ float red[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = a.E;
+#pragma unroll
+    for (int i = 0; i < kLossCols; ++i) {
+        const int c = wave + 16 * i;
+        if (c < E + 2) {
+            float sum = 0.f;
+            sum += r.v[i];
+            sum = gl_wave_sum(sum);
+            if (lane == 0) col[c] = sum;
+        }
+    }
+    __syncthreads();
+    const float fn = (float)a.N;
+    float d = 0.f;
+    if (tid < E) {
+        d = col[tid] / fn - 1.f / (float)E;
+        d = d * d;
+    }
+    d = gl_wave_sum(d);
+    if (lane == 0) red[wave] = d;
+    __syncthreads();
+    if (tid == 0) {
+        float lb = red[0];
+        for (int w = 1; w < 16; ++w) lb += red[w];
+        float total = a.lb_alpha * lb + a.cap_loss + a.z_alpha * (col[E] / ((float)a.N * (float)E));
+        if (a.has_soft) {
+            const float ac = col[E + 1] / fn - a.budget;
+            total += 0.01f * (ac * ac);
+        }
+        a.loss[0] = total;
+    }
+}
+
 }  // namespace
 }  // namespace yvmoe

@@ -552,9 +552,15 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
     const int nslots = N * k;
     const int nchunks = (nslots + 63) / 64;
 
-    // the YvMoEGate loss first: its per-work-group sums sit in the gate's workspace region,
-    // which the tile table below may overwrite
-    if (a.has_loss) {
+    // the YvMoEGate loss: its per-work-group sums sit in the gate's workspace region, which the
+    // tile table below may overwrite, so they are read before it is written — at decode sizes
+    // (at most 64 groups) their loads go out with this kernel's first ones and the sums run after
+    // the first barrier that follows; otherwise the whole loss first
+    const bool early_loss = a.has_loss && a.loss.G <= 64;
+    LossRegs lr;
+    if (early_loss) {
+        gate_loss_load(a.loss, lr);
+    } else if (a.has_loss) {
         gate_loss_block(a.loss);
         __syncthreads();
     }
@@ -571,6 +577,8 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
     }
     if (a.cap_mode == 2 && tid < kSmallRouteTok) s_score[tid] = tid < N ? a.score[tid] : 0.0f;
     __syncthreads();
+    // (barriers inside; the loss partial sums are all read before the tile table is written)
+    if (early_loss) gate_loss_finish(a.loss, lr);
 
     // stable scatter, part 1: rank within a 64-slot chunk from 8 ballots over the expert id
     // bits (all waves); counts, offsets and capacity (wave 0, after its chunks)
