@@ -530,6 +530,9 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
     return v;
 }
 
+// EARLY_LOSS: the launch with the YvMoEGate loss over at most 64 groups (an instance of its own,
+// so the other launches keep their registers and schedule).
+template <bool EARLY_LOSS>
 __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
     __shared__ int hist[YVMOE_MAX_EXPERTS];
     __shared__ int s_off[YVMOE_MAX_EXPERTS + 1];
@@ -556,9 +559,8 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
     // tile table below may overwrite, so they are read before it is written — at decode sizes
     // (at most 64 groups) their loads go out with this kernel's first ones and the sums run after
     // the first barrier that follows; otherwise the whole loss first
-    const bool early_loss = a.has_loss && a.loss.G <= 64;
     LossRegs lr;
-    if (early_loss) {
+    if constexpr (EARLY_LOSS) {
         gate_loss_load(a.loss, lr);
     } else if (a.has_loss) {
         gate_loss_block(a.loss);
@@ -578,7 +580,7 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
     if (a.cap_mode == 2 && tid < kSmallRouteTok) s_score[tid] = tid < N ? a.score[tid] : 0.0f;
     __syncthreads();
     // (barriers inside; the loss partial sums are all read before the tile table is written)
-    if (early_loss) gate_loss_finish(a.loss, lr);
+    if constexpr (EARLY_LOSS) gate_loss_finish(a.loss, lr);
 
     // stable scatter, part 1: rank within a 64-slot chunk from 8 ballots over the expert id
     // bits (all waves); counts, offsets and capacity (wave 0, after its chunks)
@@ -887,7 +889,10 @@ int route_launch(const float* logits, int ld, const float* pred, int pred_ld, in
             a.has_loss = 1;
             a.loss = *loss;
         }
-        route_small_kernel<<<1, 1024, 0, st>>>(a);
+        if (a.has_loss && a.loss.G <= 64)
+            route_small_kernel<true><<<1, 1024, 0, st>>>(a);
+        else
+            route_small_kernel<false><<<1, 1024, 0, st>>>(a);
         YV_LAUNCH_CHECK("route_small");
         return YVMOE_OK;
     }
