@@ -77,15 +77,26 @@ __device__ __forceinline__ void gate_loss_block(const GateLossArgs& a) {
     }
 }
 
-// Split form of gate_loss_block for at most 64 groups (the small-batch routing kernel): the
-// loads go out with the caller's first loads (gate_loss_load, lane l of wavefront w holding
-// group l of columns w, w + 16, ...), and the sums run later (gate_loss_finish, every thread,
-// barriers inside) with gate_loss_block's arithmetic: each column's sum is 0 + its lane's value
-// (gate_loss_block's further terms are zeros at this size), then the same wave reduction.
+// Split form of gate_loss_block for at most 64 groups (the small-batch routing kernel), its
+// phases placed between the caller's own barriers: gate_loss_load issues the loads with the
+// caller's first loads (lane l of wavefront w holds group l of columns w, w + 16, ...);
+// gate_loss_cols (after a barrier that follows the loads; every thread) sums the columns into
+// LDS; gate_loss_lb (after a later barrier; every thread) adds the load-balance terms per
+// wavefront; gate_loss_total (after a later barrier; one thread) writes the loss. The arithmetic
+// is gate_loss_block's: each column's sum is 0 + its lane's value (gate_loss_block's further
+// terms are zeros at this size), then the same wave reductions and the waves in order.
 constexpr int kLossCols = (YVMOE_MAX_EXPERTS + 2 + 15) / 16;
 struct LossRegs {
     float v[kLossCols];
 };
+struct LossLds {
+    float col[YVMOE_MAX_EXPERTS + 2];
+    float red[16];
+};
+__device__ __forceinline__ LossLds& loss_lds() {
+    __shared__ LossLds s;
+    return s;
+}
 __device__ __forceinline__ void gate_loss_load(const GateLossArgs& a, LossRegs& r) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
@@ -94,41 +105,44 @@ __device__ __forceinline__ void gate_loss_load(const GateLossArgs& a, LossRegs& 
         r.v[i] = (c < a.E + 2 && lane < a.G) ? a.part[(long long)c * a.G + lane] : 0.f;
     }
 }
-__device__ __forceinline__ void gate_loss_finish(const GateLossArgs& a, const LossRegs& r) {
-    __shared__ float col[YVMOE_MAX_EXPERTS + 2];
-    __shared__ float red[16];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int E = a.E;
+__device__ __forceinline__ void gate_loss_cols(const GateLossArgs& a, const LossRegs& r) {
+    LossLds& l = loss_lds();
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int i = 0; i < kLossCols; ++i) {
         const int c = wave + 16 * i;
-        if (c < E + 2) {
+        if (c < a.E + 2) {
             float sum = 0.f;
             sum += r.v[i];
             sum = gl_wave_sum(sum);
-            if (lane == 0) col[c] = sum;
+            if (lane == 0) l.col[c] = sum;
         }
     }
-    __syncthreads();
-    const float fn = (float)a.N;
+}
+__device__ __forceinline__ void gate_loss_lb(const GateLossArgs& a) {
+    LossLds& l = loss_lds();
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = a.E;
     float d = 0.f;
     if (tid < E) {
-        d = col[tid] / fn - 1.f / (float)E;
+        d = l.col[tid] / (float)a.N - 1.f / (float)E;
         d = d * d;
     }
     d = gl_wave_sum(d);
-    if (lane == 0) red[wave] = d;
-    __syncthreads();
-    if (tid == 0) {
-        float lb = red[0];
-        for (int w = 1; w < 16; ++w) lb += red[w];
-        float total = a.lb_alpha * lb + a.cap_loss + a.z_alpha * (col[E] / ((float)a.N * (float)E));
-        if (a.has_soft) {
-            const float ac = col[E + 1] / fn - a.budget;
-            total += 0.01f * (ac * ac);
-        }
-        a.loss[0] = total;
+    if (lane == 0) l.red[wave] = d;
+}
+__device__ __forceinline__ void gate_loss_total(const GateLossArgs& a) {
+    const LossLds& l = loss_lds();
+    const int E = a.E;
+    const float fn = (float)a.N;
+    float lb = l.red[0];
+    for (int w = 1; w < 16; ++w) lb += l.red[w];
+    float total = a.lb_alpha * lb + a.cap_loss + a.z_alpha * (l.col[E] / ((float)a.N * (float)E));
+    if (a.has_soft) {
+        const float ac = l.col[E + 1] / fn - a.budget;
+        total += 0.01f * (ac * ac);
     }
+    a.loss[0] = total;
 }
 
 }  // namespace

@@ -557,8 +557,8 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
 
     // the YvMoEGate loss: its per-work-group sums sit in the gate's workspace region, which the
     // tile table below may overwrite, so they are read before it is written — at decode sizes
-    // (at most 64 groups) their loads go out with this kernel's first ones and the sums run after
-    // the first barrier that follows; otherwise the whole loss first
+    // (at most 64 groups) their loads go out with this kernel's first ones and the sums run
+    // between the routing's own barriers; otherwise the whole loss first
     LossRegs lr;
     if constexpr (EARLY_LOSS) {
         gate_loss_load(a.loss, lr);
@@ -579,8 +579,8 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
     }
     if (a.cap_mode == 2 && tid < kSmallRouteTok) s_score[tid] = tid < N ? a.score[tid] : 0.0f;
     __syncthreads();
-    // (barriers inside; the loss partial sums are all read before the tile table is written)
-    if constexpr (EARLY_LOSS) gate_loss_finish(a.loss, lr);
+    // (the loss partial sums are all read here, before the tile table is written)
+    if constexpr (EARLY_LOSS) gate_loss_cols(a.loss, lr);
 
     // stable scatter, part 1: rank within a 64-slot chunk from 8 ballots over the expert id
     // bits (all waves); counts, offsets and capacity (wave 0, after its chunks)
@@ -664,6 +664,7 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
             run += v;
         }
     }
+    if constexpr (EARLY_LOSS) gate_loss_lb(a.loss);
     __syncthreads();
     for (int s = tid; s < nslots; s += 1024) {
         const int e = s_idx[s];
@@ -737,7 +738,10 @@ __global__ __launch_bounds__(1024) void route_small_kernel(SmallRouteArgs a) {
     __syncthreads();
 
     // weights: renormalised over the kept slots (renorm_kernel), or the first softmax
-    // unchanged in fixed-shape mode
+    // unchanged in fixed-shape mode; the loss by the last thread (at most 256 tokens here)
+    if constexpr (EARLY_LOSS) {
+        if (tid == 1023) gate_loss_total(a.loss);
+    }
     if (tid < N) {
         const int t = tid;
         if (a.cap_mode != 0) {
