@@ -3,7 +3,7 @@
 //          + 0.01 · (mean_n Σ_e soft - budget)²
 // part holds E + 2 columns of G per-work-group sums (scores per expert, Σ logits², Σ soft).
 // Run by one work-group of 1024 threads: its own kernel after the per-token kernels
-// (yvmoe_moegate.hip), or the tail of the small-batch routing kernel (yvmoe_route.hip), which
+// (yvmoe_moegate.hip), or inside the small-batch routing kernel (yvmoe_route.hip), which
 // runs next on the stream at decode sizes — the same arithmetic either way. Column c is summed
 // by one wavefront (lane l takes groups l, l + 64, ... in order, then a wave reduction: the
 // loads of a step are one coalesced 256-byte row; the earlier layout, P threads per column over
